@@ -1,0 +1,342 @@
+"""Benchmark of the MI355X shifted-window hot path (one GPU).
+
+A step is one pass of the hot path over one batch: the shift-partition plus
+unshift-unpartition round trip of BASELINE config 1 ([1, 98^3, 48] fp16,
+window 7, shift 3), called through the public crumpet API with the input
+resident in HBM.  ``value`` is the round trip's algorithmic bytes
+(2 x 180,708,864 B) per step time, in GB/s.
+
+The same run also measures, each on its own BASELINE config:
+  * the partition and unpartition kernels alone (per-launch HIP events,
+    rotating buffer sets so no launch reads what the 256 MB MALL still holds);
+  * the mask kernel (config 2, 98^3 fp16, 645,657,712 B written);
+  * fused window attention (config 3, 1372 windows x 3 heads, N=343, hd 16),
+    in TFLOP/s, with the eager ROCm PyTorch chain timed beside it;
+  * the CPU oracle on the host cores as the reported CPU baseline.
+
+Prints ONE JSON line.  Only one GPU is supported: --gpus above 1 exits.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+C1 = dict(B=1, D=98, H=98, W=98, C=48, ws=(7, 7, 7), ss=(3, 3, 3))
+C1_BYTES = 2 * 1 * 98 * 98 * 98 * 48 * 2  # read + write per direction: 180,708,864
+C2_BYTES = 2744 * 343 * 343 * 2  # 645,657,712
+C3 = dict(B=1372, H=3, N=343, Dh=16, D=49)
+C3_FLOPS = 4 * 343 * 343 * 16 * 3 * 1372  # 30,991,570,176
+C3_BYTES = 1372 * 343 * 144 * 2 + 1372 * 343 * 48 * 2  # qkv in + out: 180,708,864
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-attention", action="store_true")
+    p.add_argument("--no-eager", action="store_true", help="skip the eager GPU attention chain")
+    p.add_argument("--profile", action="store_true",
+                   help="short fixed launch sequence for rocprofv3 (plus a copy of known size)")
+    return p.parse_args()
+
+
+def _events_time(fn, iters):
+    """Average ms per call of fn over iters back-to-back calls, HIP events on the current stream."""
+    import torch
+
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for i in range(iters):
+        fn(i)
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def seeded(shape, dtype, seed):
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g, dtype=torch.float32).to(dtype)
+
+
+def bench_partition(args, dev):
+    import torch
+
+    import crumpet_amd
+
+    ops = torch.ops.crumpet_ops
+    B, D, H, W, C, ws, ss = (C1[k] for k in ("B", "D", "H", "W", "C", "ws", "ss"))
+    R = 4  # 4 x 180 MB rotating sets > 256 MB MALL
+    xs = [seeded((B, D, H, W, C), torch.float16, 100 + r).to(dev) for r in range(R)]
+    wins = [torch.empty((B * 2744, 343, C), dtype=torch.float16, device=dev) for _ in range(R)]
+    backs = [torch.empty_like(xs[0]) for _ in range(R)]
+
+    # correctness gate on the measured buffers: round trip restores the input
+    w0 = crumpet_amd.fused_shift_partition_3d(xs[0], ws, ss)
+    assert torch.equal(crumpet_amd.fused_unshift_unpartition_3d(w0, B, D, H, W, C, ws, ss), xs[0])
+    del w0
+
+    def part(i):
+        ops.fused_shift_partition_3d(wins[i % R], xs[i % R], *ws, *ss)
+
+    def unpart(i):
+        ops.fused_unshift_unpartition_3d(backs[i % R], wins[i % R], B, D, H, W, C, *ws, *ss)
+
+    def step(i):
+        w = crumpet_amd.fused_shift_partition_3d(xs[i % R], ws, ss)
+        crumpet_amd.fused_unshift_unpartition_3d(w, B, D, H, W, C, ws, ss)
+
+    for fn in (part, unpart, step):
+        _events_time(fn, args.warmup)
+    t_part = _events_time(part, args.steps)
+    t_unpart = _events_time(unpart, args.steps)
+    t_step = _events_time(step, args.steps)
+    return dict(t_part=t_part, t_unpart=t_unpart, t_step=t_step)
+
+
+def bench_mask(args, dev):
+    import torch
+
+    ops = torch.ops.crumpet_ops
+    out = torch.empty((2744, 343, 343), dtype=torch.float16, device=dev)
+
+    def mk(i):
+        ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
+
+    _events_time(mk, args.warmup)
+    return _events_time(mk, args.steps)
+
+
+def c3_inputs(dev, sets):
+    import torch
+
+    from crumpet_amd import compute_attn_mask_3d
+
+    B, H, N, Dh = C3["B"], C3["H"], C3["N"], C3["Dh"]
+    qkvs = [seeded((B, N, 3 * H * Dh), torch.float16, 300 + r).to(dev) for r in range(sets)]
+    g = torch.Generator().manual_seed(310)
+    table = torch.empty((2197, H))
+    torch.nn.init.trunc_normal_(table, std=0.02, a=-2.0, b=2.0, generator=g)
+    import numpy as np
+
+    c = np.stack(np.meshgrid(np.arange(7), np.arange(7), np.arange(7), indexing="ij")).reshape(3, -1)
+    rel = (c[:, :, None] - c[:, None, :]) + 6
+    rpi = torch.from_numpy((rel[0] * 13 + rel[1]) * 13 + rel[2])
+    bias = table[rpi.reshape(-1)].reshape(N, N, H).permute(2, 0, 1).contiguous().half().to(dev)
+    mask = compute_attn_mask_3d(C3["D"], C3["D"], C3["D"], (7, 7, 7), (3, 3, 3), torch.float16, dev)
+    nw = mask.shape[0]
+    flags = (mask.view(nw, -1).abs().amax(1) > 0).to(torch.uint8)
+    bnd = flags.repeat(B // nw).contiguous()
+    return qkvs, bias, mask, bnd
+
+
+def bench_attention(args, dev):
+    import torch
+
+    from crumpet_amd.fused_attention import fused_swin_attention_windows
+
+    B, H, N, Dh = C3["B"], C3["H"], C3["N"], C3["Dh"]
+    R = 3  # 3 x 180 MB rotating sets > 256 MB MALL
+    qkvs, bias, mask, bnd = c3_inputs(dev, R)
+    views = [q.reshape(B, N, 3, H, Dh).permute(2, 0, 3, 1, 4) for q in qkvs]
+    outs = [torch.empty((B, N, H * Dh), dtype=torch.float16, device=dev) for _ in range(R)]
+    ovs = [o.view(B, N, H, Dh).permute(0, 2, 1, 3) for o in outs]
+
+    def attn(i):
+        t = views[i % R]
+        fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ovs[i % R])
+
+    _events_time(attn, args.warmup)
+    t_attn = _events_time(attn, args.steps)
+    res = dict(t_attn=t_attn)
+
+    # accuracy on a sample of windows vs fp32 torch (GPU) of the same inputs
+    t = views[0]
+    attn(0)
+    torch.cuda.synchronize()
+    idx = torch.arange(0, B, 7, device=dev)
+    qf, kf, vf = (t[j][idx].float() for j in range(3))
+    s = (qf * 0.25) @ kf.transpose(-1, -2).contiguous() + bias.float()[None]
+    mb = (mask.float()[idx % mask.shape[0]] * bnd[idx].float()[:, None, None])[:, None]
+    ref = torch.softmax(s + mb, dim=-1) @ vf
+    res["max_abs_err"] = float((ovs[0][idx].float() - ref).abs().max())
+    del qf, kf, vf, s, mb, ref
+
+    if not args.no_eager:
+        # MONAI eager chain in fp16 on the same GPU (the "eager ROCm PyTorch" comparison)
+        def eager(i):
+            tt = views[i % R]
+            q = tt[0] * 0.25
+            a = q @ tt[1].transpose(-2, -1).contiguous()
+            a = a + bias.unsqueeze(0)
+            nw = mask.shape[0]
+            a = a.view(B // nw, nw, H, N, N) + mask.unsqueeze(1).unsqueeze(0)
+            a = torch.softmax(a.view(-1, H, N, N), dim=-1)
+            return (a @ tt[2]).transpose(1, 2).reshape(B, N, H * Dh)
+
+        with torch.no_grad():
+            _events_time(eager, 2)
+            res["t_eager"] = _events_time(eager, max(3, min(args.steps, 10)))
+        torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline():
+    """Oracle (C scalar, 1 thread) round trip on the full config-1 volume."""
+    import numpy as np
+
+    from oracle import oracle
+
+    oracle.build_oracle()
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((1, 98, 98, 98, 48)).astype(np.float16)
+    oracle.shift_partition(x, (7, 7, 7), (3, 3, 3))  # warm
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        w = oracle.shift_partition(x, (7, 7, 7), (3, 3, 3))
+        oracle.unshift_unpartition(w, 1, 98, 98, 98, 48, (7, 7, 7), (3, 3, 3))
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 50:
+            break
+    gbs = 2 * C1_BYTES * reps / el / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"full config-1 round trip ([1,98^3,48] fp16) x{reps}, oracle/crumpet_oracle.c scalar, {el:.1f} s"}
+
+
+def profile_run(dev):
+    """Fixed short sequence for rocprofv3: 10 launches of each kernel plus a
+    plain 256 MiB device copy (read 256 MiB + write 256 MiB) for scaling the
+    FETCH_SIZE / WRITE_SIZE counters."""
+    import torch
+
+    ops = torch.ops.crumpet_ops
+    B, D, H, W, C, ws, ss = (C1[k] for k in ("B", "D", "H", "W", "C", "ws", "ss"))
+    R = 4
+    xs = [seeded((B, D, H, W, C), torch.float16, 100 + r).to(dev) for r in range(R)]
+    wins = [torch.empty((2744, 343, C), dtype=torch.float16, device=dev) for _ in range(R)]
+    backs = [torch.empty_like(xs[0]) for _ in range(R)]
+    src = torch.ones((1 << 27,), dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    for i in range(10):
+        ops.fused_shift_partition_3d(wins[i % R], xs[i % R], *ws, *ss)
+    for i in range(10):
+        ops.fused_unshift_unpartition_3d(backs[i % R], wins[i % R], B, D, H, W, C, *ws, *ss)
+    out = torch.empty((2744, 343, 343), dtype=torch.float16, device=dev)
+    for i in range(10):
+        ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
+    for i in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del out
+    from crumpet_amd.fused_attention import fused_swin_attention_windows
+
+    qkvs, bias, mask, bnd = c3_inputs(dev, 3)
+    Bw, Hh, N, Dh = C3["B"], C3["H"], C3["N"], C3["Dh"]
+    o = torch.empty((Bw, N, Hh * Dh), dtype=torch.float16, device=dev)
+    ov = o.view(Bw, N, Hh, Dh).permute(0, 2, 1, 3)
+    for i in range(10):
+        t = qkvs[i % 3].reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4)
+        fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ov)
+    torch.cuda.synchronize()
+    print("profile sequence done", flush=True)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); "
+              "the shifted-window path is single-GPU in this build", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import crumpet_amd
+
+    if not crumpet_amd._HAS_HIP_EXT:
+        raise RuntimeError(f"crumpet_amd HIP extension missing: {crumpet_amd._native.load_error()}")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.profile:
+        profile_run(dev)
+        return
+
+    p = bench_partition(args, dev)
+    t_mask = bench_mask(args, dev)
+    torch.cuda.empty_cache()
+    a = {} if args.no_attention else bench_attention(args, dev)
+    torch.cuda.empty_cache()
+
+    gbs_step = 2 * C1_BYTES / (p["t_step"] * 1e-3) / 1e9
+    gbs_part = C1_BYTES / (p["t_part"] * 1e-3) / 1e9
+    gbs_unpart = C1_BYTES / (p["t_unpart"] * 1e-3) / 1e9
+    gbs_mask = C2_BYTES / (t_mask * 1e-3) / 1e9
+    components = {
+        "partition": {"ms": round(p["t_part"], 5), "GB_s": round(gbs_part, 1),
+                      "frac_hbm": round(gbs_part / HBM_PEAK_GBS, 4), "bytes": C1_BYTES},
+        "unpartition": {"ms": round(p["t_unpart"], 5), "GB_s": round(gbs_unpart, 1),
+                        "frac_hbm": round(gbs_unpart / HBM_PEAK_GBS, 4), "bytes": C1_BYTES},
+        "mask": {"ms": round(t_mask, 5), "GB_s": round(gbs_mask, 1),
+                 "frac_hbm": round(gbs_mask / HBM_PEAK_GBS, 4), "bytes": C2_BYTES,
+                 "workload": "config 2: 98^3 fp16 ws7 ss3 -> [2744,343,343]"},
+    }
+    if a:
+        tfl = C3_FLOPS / (a["t_attn"] * 1e-3) / 1e12
+        comp = {"ms": round(a["t_attn"], 5), "TFLOP_s": round(tfl, 2),
+                "frac_mfma_f16": round(tfl / MFMA_F16_PEAK_TFLOPS, 4),
+                "GB_s": round(C3_BYTES / (a["t_attn"] * 1e-3) / 1e9, 1),
+                "frac_hbm": round(C3_BYTES / (a["t_attn"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                "flops": C3_FLOPS, "bytes": C3_BYTES, "max_abs_err_vs_fp32": a["max_abs_err"],
+                "workload": "config 3: 1372 windows x 3 heads, N=343, hd16, fp16, shifted 49^3 mask"}
+        if "t_eager" in a:
+            comp["eager_rocm_ms"] = round(a["t_eager"], 4)
+            comp["speedup_vs_eager"] = round(a["t_eager"] / a["t_attn"], 2)
+        components["attention"] = comp
+
+    line = {
+        "metric": "partition/unpartition GB/s (% HBM peak); window-attn TFLOP/s; ms per 96³ fwd",
+        "value": round(gbs_step, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(p["t_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic: seeded N(0,1) fp16 volumes generated on the CPU",
+        "config": {"workload": "config 1: shift-partition + unshift-unpartition round trip, "
+                               "[1,98,98,98,48] fp16, window (7,7,7), shift (3,3,3)",
+                   "bytes_per_step": 2 * C1_BYTES, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs_part, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs_part / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel": "window_gather_kernel (shift-partition)",
+                     "avg_launch_ms": round(p["t_part"], 5)},
+        "components": components,
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline()
+    line["cpu_baseline_threads"] = {"os_cpu_count": os.cpu_count(),
+                                    "torch_threads": torch.get_num_threads()}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,227 @@
+// Dispatcher registration of the crumpet_ops operators on ROCm PyTorch.
+//
+// Same five op schemas and tags as the reference
+// (torch-ext/torch_binding.cpp:10-31), plus `fused_swin_attention`, which
+// the reference launched from Python through Triton.  Every impl checks
+// shapes, dtypes and devices (so no launch can index outside its tensors),
+// takes the current HIP stream of the tensor's device and forwards to the
+// C ABI of libcrumpet_hip.so (include/crumpet_hip.h).  A non-OK status
+// becomes a RuntimeError carrying crumpet_last_error().
+#include <ATen/core/Tensor.h>
+#include <ATen/ops/empty.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+#include <torch/library.h>
+
+#include "crumpet_hip.h"
+
+namespace {
+
+const std::vector<at::Tag> kCrumpetOpTags = {
+    at::Tag::pt2_compliant_tag,
+    at::Tag::needs_fixed_stride_order,
+};
+
+void* stream_of(const at::Tensor& t) {
+    return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+}
+
+void check_status(int status) {
+    TORCH_CHECK(status == CRUMPET_OK, "crumpet_ops: ", crumpet_last_error(), " (",
+                crumpet_status_string(status), ")");
+}
+
+void check_device_pair(const at::Tensor& out, const at::Tensor& in, const char* what) {
+    TORCH_CHECK(out.is_cuda() && in.is_cuda(), what, ": tensors must be on a HIP device");
+    TORCH_CHECK(out.device() == in.device(), what, ": tensors must be on the same device");
+    TORCH_CHECK(out.scalar_type() == in.scalar_type(), what, ": dtype mismatch");
+    TORCH_CHECK(out.is_contiguous() && in.is_contiguous(), what, ": tensors must be contiguous");
+    TORCH_CHECK(out.numel() == in.numel(), what, ": output and input sizes differ");
+}
+
+int32_t dtype_code(at::ScalarType t) {
+    switch (t) {
+        case at::kFloat: return CRUMPET_DTYPE_F32;
+        case at::kHalf: return CRUMPET_DTYPE_F16;
+        case at::kBFloat16: return CRUMPET_DTYPE_BF16;
+        default: return -1;
+    }
+}
+
+void compute_attn_mask_3d(at::Tensor& output, int64_t D, int64_t H, int64_t W, int64_t ws_d,
+                          int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w) {
+    TORCH_CHECK(output.is_cuda(), "compute_attn_mask_3d: output must be on a HIP device");
+    const c10::hip::HIPGuard guard(output.device());
+    if (output.numel() == 0) return;
+    const int32_t dt = dtype_code(output.scalar_type());
+    TORCH_CHECK(dt >= 0, "compute_attn_mask_3d: output dtype must be float32, float16 or bfloat16");
+    TORCH_CHECK(output.is_contiguous(), "compute_attn_mask_3d: output must be contiguous");
+    TORCH_CHECK(ws_d > 0 && ws_h > 0 && ws_w > 0 && D % ws_d == 0 && H % ws_h == 0 && W % ws_w == 0,
+                "compute_attn_mask_3d: D, H and W must be divisible by window_size");
+    const int64_t vol = ws_d * ws_h * ws_w;
+    const int64_t nW = (D / ws_d) * (H / ws_h) * (W / ws_w);
+    TORCH_CHECK(output.numel() == nW * vol * vol, "compute_attn_mask_3d: output must hold ", nW,
+                " x ", vol, " x ", vol, " elements");
+    check_status(crumpet_compute_attn_mask_3d(output.data_ptr(), dt, D, H, W, ws_d, ws_h, ws_w,
+                                              ss_d, ss_h, ss_w, stream_of(output)));
+}
+
+void fused_shift_partition_3d(at::Tensor& output, const at::Tensor& x, int64_t ws_d, int64_t ws_h,
+                              int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w) {
+    TORCH_CHECK(x.dim() == 5, "fused_shift_partition_3d: x must have shape [B, D, H, W, C]");
+    check_device_pair(output, x, "fused_shift_partition_3d");
+    const c10::hip::HIPGuard guard(x.device());
+    if (output.numel() == 0) return;
+    check_status(crumpet_shift_partition_3d(output.data_ptr(), x.data_ptr(), x.size(0), x.size(1),
+                                            x.size(2), x.size(3), x.size(4), x.element_size(),
+                                            ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, stream_of(x)));
+}
+
+void fused_unshift_unpartition_3d(at::Tensor& output, const at::Tensor& windows, int64_t B,
+                                  int64_t D, int64_t H, int64_t W, int64_t C, int64_t ws_d,
+                                  int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h,
+                                  int64_t ss_w) {
+    check_device_pair(output, windows, "fused_unshift_unpartition_3d");
+    const c10::hip::HIPGuard guard(windows.device());
+    if (output.numel() == 0) return;
+    TORCH_CHECK(output.numel() == B * D * H * W * C,
+                "fused_unshift_unpartition_3d: output must hold B*D*H*W*C elements");
+    check_status(crumpet_unshift_unpartition_3d(output.data_ptr(), windows.data_ptr(), B, D, H, W,
+                                                C, windows.element_size(), ws_d, ws_h, ws_w, ss_d,
+                                                ss_h, ss_w, stream_of(windows)));
+}
+
+void fused_shift_partition_3d_backward(at::Tensor& grad_x, const at::Tensor& grad_windows,
+                                       int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                       int64_t ws_d, int64_t ws_h, int64_t ws_w, int64_t ss_d,
+                                       int64_t ss_h, int64_t ss_w) {
+    check_device_pair(grad_x, grad_windows, "fused_shift_partition_3d_backward");
+    const c10::hip::HIPGuard guard(grad_windows.device());
+    if (grad_x.numel() == 0) return;
+    TORCH_CHECK(grad_x.numel() == B * D * H * W * C,
+                "fused_shift_partition_3d_backward: grad_x must hold B*D*H*W*C elements");
+    check_status(crumpet_shift_partition_3d_backward(
+        grad_x.data_ptr(), grad_windows.data_ptr(), B, D, H, W, C, grad_windows.element_size(),
+        ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, stream_of(grad_windows)));
+}
+
+void fused_unshift_unpartition_3d_backward(at::Tensor& grad_windows, const at::Tensor& grad_x,
+                                           int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                           int64_t ss_d, int64_t ss_h, int64_t ss_w) {
+    TORCH_CHECK(grad_x.dim() == 5,
+                "fused_unshift_unpartition_3d_backward: grad_x must have shape [B, D, H, W, C]");
+    check_device_pair(grad_windows, grad_x, "fused_unshift_unpartition_3d_backward");
+    const c10::hip::HIPGuard guard(grad_x.device());
+    if (grad_windows.numel() == 0) return;
+    check_status(crumpet_unshift_unpartition_3d_backward(
+        grad_windows.data_ptr(), grad_x.data_ptr(), grad_x.size(0), grad_x.size(1),
+        grad_x.size(2), grad_x.size(3), grad_x.size(4), grad_x.element_size(), ws_d, ws_h, ws_w,
+        ss_d, ss_h, ss_w, stream_of(grad_x)));
+}
+
+void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
+                          const at::Tensor& v, const at::Tensor& bias,
+                          const std::optional<at::Tensor>& mask,
+                          const std::optional<at::Tensor>& boundary, double scale) {
+    const char* what = "fused_swin_attention";
+    TORCH_CHECK(q.dim() == 4, what, ": q must have shape [B, H, N, D]");
+    TORCH_CHECK(k.sizes() == q.sizes() && v.sizes() == q.sizes() && out.sizes() == q.sizes(), what,
+                ": q, k, v and out must have the same shape");
+    TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type() &&
+                    out.scalar_type() == q.scalar_type(),
+                what, ": q, k, v and out must have the same dtype");
+    const int32_t dt = dtype_code(q.scalar_type());
+    TORCH_CHECK(dt >= 0, what, ": dtype must be float32, float16 or bfloat16");
+    const at::Device dev = q.device();
+    TORCH_CHECK(q.is_cuda() && k.device() == dev && v.device() == dev && out.device() == dev &&
+                    bias.device() == dev,
+                what, ": all tensors must be on the same HIP device");
+    const int64_t B = q.size(0), Hh = q.size(1), N = q.size(2), Dh = q.size(3);
+    TORCH_CHECK(bias.dim() == 3 && bias.size(0) == Hh && bias.size(1) == N && bias.size(2) == N,
+                what, ": relative_position_bias must have shape [H, N, N]");
+    const int32_t bdt = dtype_code(bias.scalar_type());
+    TORCH_CHECK(bdt >= 0, what, ": bias dtype must be float32, float16 or bfloat16");
+    const void* mptr = nullptr;
+    int32_t mdt = 0;
+    int64_t mbatch = 1;
+    int64_t ms[3] = {0, 0, 0};
+    if (mask.has_value()) {
+        const at::Tensor& m = *mask;
+        TORCH_CHECK(m.device() == dev, what, ": mask must be on the same device");
+        TORCH_CHECK(m.dim() == 3 && m.size(1) == N && m.size(2) == N, what,
+                    ": mask must have shape [M, N, N]");
+        mdt = dtype_code(m.scalar_type());
+        TORCH_CHECK(mdt >= 0, what, ": mask dtype must be float32, float16 or bfloat16");
+        mbatch = m.size(0);
+        TORCH_CHECK(mbatch > 0 && B % mbatch == 0, what, ": mask batch ", mbatch,
+                    " must divide the window batch ", B);
+        for (int i = 0; i < 3; ++i) ms[i] = m.stride(i);
+        if (mbatch == 1) ms[0] = 0;
+        mptr = m.data_ptr();
+    }
+    const uint8_t* bptr = nullptr;
+    if (boundary.has_value()) {
+        const at::Tensor& bd = *boundary;
+        TORCH_CHECK(bd.device() == dev, what, ": boundary must be on the same device");
+        TORCH_CHECK(bd.scalar_type() == at::kByte || bd.scalar_type() == at::kBool, what,
+                    ": boundary must be uint8 or bool");
+        TORCH_CHECK(bd.dim() == 1 && bd.size(0) == B && bd.is_contiguous(), what,
+                    ": boundary must be a contiguous [B] tensor");
+        bptr = static_cast<const uint8_t*>(bd.data_ptr());
+    }
+    const c10::hip::HIPGuard guard(dev);
+    if (out.numel() == 0) return;
+    const size_t ws_bytes = crumpet_fused_swin_attention_workspace_size(Hh, N);
+    at::Tensor ws = at::empty({static_cast<int64_t>((ws_bytes + 15) / 16) * 4},
+                              q.options().dtype(at::kFloat));
+    int64_t qs[4], ks[4], vs[4], os[4], bs[3];
+    for (int i = 0; i < 4; ++i) {
+        qs[i] = q.stride(i);
+        ks[i] = k.stride(i);
+        vs[i] = v.stride(i);
+        os[i] = out.stride(i);
+    }
+    for (int i = 0; i < 3; ++i) bs[i] = bias.stride(i);
+    check_status(crumpet_fused_swin_attention(
+        out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
+        bias.data_ptr(), bdt, bs, mptr, mdt, mbatch, ms, bptr, static_cast<float>(scale),
+        ws.data_ptr(), ws_bytes, stream_of(q)));
+}
+
+}  // namespace
+
+TORCH_LIBRARY(crumpet_ops, ops) {
+    ops.def(
+        "compute_attn_mask_3d(Tensor! output, int D, int H, int W, int ws_d, int ws_h, int ws_w, "
+        "int ss_d, int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
+    ops.def(
+        "fused_shift_partition_3d(Tensor! output, Tensor x, int ws_d, int ws_h, int ws_w, "
+        "int ss_d, int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
+    ops.def(
+        "fused_shift_partition_3d_backward(Tensor! grad_x, Tensor grad_windows, int B, int D, "
+        "int H, int W, int C, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
+    ops.def(
+        "fused_unshift_unpartition_3d(Tensor! output, Tensor windows, int B, int D, int H, int W, "
+        "int C, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
+    ops.def(
+        "fused_unshift_unpartition_3d_backward(Tensor! grad_windows, Tensor grad_x, int ws_d, "
+        "int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
+    ops.def(
+        "fused_swin_attention(Tensor! out, Tensor q, Tensor k, Tensor v, Tensor bias, "
+        "Tensor? mask, Tensor? boundary, float scale) -> ()",
+        kCrumpetOpTags);
+}
+
+TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
+    ops.impl("compute_attn_mask_3d", &compute_attn_mask_3d);
+    ops.impl("fused_shift_partition_3d", &fused_shift_partition_3d);
+    ops.impl("fused_shift_partition_3d_backward", &fused_shift_partition_3d_backward);
+    ops.impl("fused_unshift_unpartition_3d", &fused_unshift_unpartition_3d);
+    ops.impl("fused_unshift_unpartition_3d_backward", &fused_unshift_unpartition_3d_backward);
+    ops.impl("fused_swin_attention", &fused_swin_attention);
+}

@@ -1,0 +1,86 @@
+"""Fused 3D Swin window attention on MI355X.
+
+``fused_swin_attention`` keeps the signature and argument semantics of the
+reference wrapper (torch-ext/crumpet/fused_attention.py:149-226); the
+computation runs in the gfx950 HIP kernel behind the
+``crumpet_ops::fused_swin_attention`` dispatcher op:
+
+    out[b, h] = softmax(q[b,h] * scale @ k[b,h]^T + bias[h]
+                        + (boundary[b] ? mask[b] : 0)) @ v[b,h]
+
+The kernel reads q, k, v through their strides (no ``.contiguous()``
+copies are needed) and writes ``out`` through its strides.  ``block_m`` and
+``block_n`` are accepted for API compatibility; the HIP kernel's tiling is
+fixed by the MFMA shape (16-query strips, 16-key tiles).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _native
+
+
+def fused_swin_attention(
+    q: torch.Tensor,  # [B, H, N, D]
+    k: torch.Tensor,  # [B, H, N, D]
+    v: torch.Tensor,  # [B, H, N, D]
+    relative_position_bias: torch.Tensor,  # [H, N, N]
+    mask: torch.Tensor | None,  # [num_windows (== B) or 1, N, N] or None
+    boundary: torch.Tensor | None = None,  # [B] uint8 / bool
+    scale: float | None = None,
+    block_m: int = 64,
+    block_n: int = 32,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Compute fused 3D Swin window attention.
+
+    ``q``, ``k``, ``v`` have shape ``[B * num_windows, num_heads, N, head_dim]``.
+    ``relative_position_bias`` is ``[num_heads, N, N]`` and broadcasts over the
+    batch.  ``mask`` is ``[B, N, N]`` or ``[1, N, N]`` (broadcast), or ``None``.
+    ``boundary`` is a per-window uint8/bool flag; a zero flag skips that
+    window's mask.  With a mask and no flags every window reads its mask.
+    ``out`` (optional, any strides, same shape/dtype as q) receives the result;
+    by default a tensor like ``q`` is allocated.
+    """
+    assert q.is_cuda and k.is_cuda and v.is_cuda
+    assert q.shape == k.shape == v.shape, "Q/K/V shape mismatch"
+    B, H, N, D = q.shape
+    assert relative_position_bias.shape == (H, N, N)
+
+    if scale is None:
+        scale = 1.0 / (D ** 0.5)
+
+    bnd = None
+    if mask is not None:
+        if mask.shape[0] != 1:
+            assert mask.shape[0] == B, f"mask shape {mask.shape[0]} incompatible with B={B}"
+        if boundary is not None:
+            bnd = boundary if boundary.dtype == torch.uint8 else boundary.to(torch.uint8)
+            bnd = bnd.contiguous()
+
+    if out is None:
+        out = torch.empty_like(q)
+    _native.ops().fused_swin_attention(out, q, k, v, relative_position_bias, mask, bnd, float(scale))
+    return out
+
+
+def fused_swin_attention_windows(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    relative_position_bias: torch.Tensor,
+    mask: torch.Tensor | None,
+    boundary: torch.Tensor | None,
+    scale: float,
+    out: torch.Tensor,
+) -> torch.Tensor:
+    """Raw form used by the MONAI integration: ``mask`` may hold one mask per
+    window position ``[nW, N, N]`` with ``nW`` dividing ``B``; window ``b``
+    then reads ``mask[b % nW]`` (the layout MONAI's ``mask.repeat`` tiling
+    produces, without materialising the repeat)."""
+    _native.ops().fused_swin_attention(out, q, k, v, relative_position_bias, mask, boundary, float(scale))
+    return out
+
+
+__all__ = ["fused_swin_attention"]

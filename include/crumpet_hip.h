@@ -1,0 +1,198 @@
+/*
+ * crumpet_hip.h - C ABI of the MI355X (gfx950) shifted-window kernels.
+ *
+ * libcrumpet_hip.so exports these entry points.  Every one of them is
+ * stateless and re-entrant: the caller owns and preallocates every buffer,
+ * passes raw device pointers plus sizes, and the work is enqueued
+ * asynchronously on `stream` (a hipStream_t; NULL means the null stream).
+ * Nothing here allocates device memory, synchronises the host or keeps
+ * global device state.
+ *
+ * Each entry point returns CRUMPET_OK or a crumpet_status code.  The
+ * human-readable reason of the last failure on the calling thread is
+ * available from crumpet_last_error().
+ *
+ * The dispatcher ops of the reference that these entry points replace are
+ * cited next to each declaration (file:line in chrisvoncsefalvay/crumpet).
+ * The torch binding in crumpet_amd/csrc/torch_binding.cpp registers the same
+ * op schemas under the `crumpet_ops` namespace and forwards to these calls.
+ */
+#ifndef CRUMPET_HIP_H_
+#define CRUMPET_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every entry point. */
+enum crumpet_status {
+    CRUMPET_OK = 0,
+    CRUMPET_ERR_INVALID_ARGUMENT = 1, /* shape, shift, dtype, stride or pointer check failed */
+    CRUMPET_ERR_UNSUPPORTED = 2,      /* valid request outside what the kernels implement */
+    CRUMPET_ERR_HIP = 3               /* the HIP runtime reported an error at launch */
+};
+
+/* Element type codes. */
+enum crumpet_dtype {
+    CRUMPET_DTYPE_F32 = 0,
+    CRUMPET_DTYPE_F16 = 1,
+    CRUMPET_DTYPE_BF16 = 2,
+    CRUMPET_DTYPE_U8 = 3 /* only for boundary flags */
+};
+
+/* Library version, e.g. "0.1.0". */
+const char* crumpet_version(void);
+
+/* Message describing the last non-OK status returned on this thread. */
+const char* crumpet_last_error(void);
+
+/* Static name of a status code. */
+const char* crumpet_status_string(int status);
+
+/*
+ * Fused cyclic shift (torch.roll by -shift over D, H, W) plus 3D window
+ * partition of a contiguous channels-last volume.
+ *
+ *   x   : [B, D, H, W, C]                      (elem_size bytes per element)
+ *   out : [B * nW, ws_d * ws_h * ws_w, C]      nW = (D/ws_d)(H/ws_h)(W/ws_w)
+ *
+ *   out[(b*nW + win)*vol + loc, c] =
+ *       x[b, (wd*ws_d+ld+ss_d) mod D, (wh*ws_h+lh+ss_h) mod H,
+ *            (ww*ws_w+lw+ss_w) mod W, c]
+ *
+ * A pure byte copy: bit-exact for every element type.  D, H, W must be
+ * divisible by the window and 0 <= ss < ws on every axis.
+ *
+ * Replaces op `fused_shift_partition_3d(Tensor! output, Tensor x, ...)`,
+ * torch-ext/torch_binding.cpp:19-21, host entry
+ * cuda/shift_partition_3d.cu:318-347.
+ */
+int crumpet_shift_partition_3d(void* out, const void* x,
+                               int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                               int64_t elem_size,
+                               int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                               int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                               void* stream);
+
+/*
+ * Inverse of crumpet_shift_partition_3d: window reverse plus torch.roll by
+ * +shift.
+ *
+ *   windows : [B * nW, vol, C]
+ *   out     : [B, D, H, W, C]
+ *
+ * Replaces op `fused_unshift_unpartition_3d(Tensor! output, Tensor windows,
+ * int B, int D, int H, int W, int C, ...)`, torch-ext/torch_binding.cpp:26-28,
+ * host entry cuda/unshift_unpartition_3d.cu:284-318.
+ */
+int crumpet_unshift_unpartition_3d(void* out, const void* windows,
+                                   int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                   int64_t elem_size,
+                                   int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                   int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                   void* stream);
+
+/*
+ * Gradient of the shift-partition.  The adjoint of a permutation is its
+ * inverse, so this is the unshift-unpartition gather applied to
+ * grad_windows [B*nW, vol, C], writing grad_x [B, D, H, W, C].
+ *
+ * Replaces op `fused_shift_partition_3d_backward`, torch-ext/torch_binding.cpp:22-24,
+ * host entry cuda/unshift_unpartition_3d.cu:320-348.
+ */
+int crumpet_shift_partition_3d_backward(void* grad_x, const void* grad_windows,
+                                        int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                        int64_t elem_size,
+                                        int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                        int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                        void* stream);
+
+/*
+ * Gradient of the unshift-unpartition: the shift-partition gather applied
+ * to grad_x [B, D, H, W, C], writing grad_windows [B*nW, vol, C].
+ *
+ * Replaces op `fused_unshift_unpartition_3d_backward`,
+ * torch-ext/torch_binding.cpp:29-31, host entry cuda/shift_partition_3d.cu:349-367.
+ */
+int crumpet_unshift_unpartition_3d_backward(void* grad_windows, const void* grad_x,
+                                            int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                            int64_t elem_size,
+                                            int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                            int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                            void* stream);
+
+/*
+ * Shifted-window additive attention mask, written densely.
+ *
+ *   out : [nW, vol, vol] of `dtype` (F32, F16 or BF16), contiguous
+ *
+ *   region(x, dim, ws, ss) = 0 if x < dim-ws; 1 if x < dim-ss; else 2
+ *   label(p) = 9*region_d + 3*region_h + region_w, at unrolled window
+ *              coordinates p = win*ws + loc (the shifted frame)
+ *   out[win, i, j] = label(i) != label(j) ? -100 : 0
+ *
+ * All-zero shift gives an all-zero mask.  vol must not exceed 1024.
+ *
+ * Replaces op `compute_attn_mask_3d(Tensor! output, int D, int H, int W, ...)`,
+ * torch-ext/torch_binding.cpp:16-18, host entry cuda/attn_mask_3d.cu:127-168.
+ */
+int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
+                                 int64_t D, int64_t H, int64_t W,
+                                 int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                 int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                 void* stream);
+
+/*
+ * Fused window attention, per window b and head h:
+ *
+ *   S = (q * scale) k^T + bias[h] + (boundary[b] ? mask[b mod mask_batch] : 0)
+ *   out = softmax_rows(S) v
+ *
+ * q, k, v, out : [B, Hh, N, Dh] with arbitrary element strides (in elements,
+ *                order b, h, n, d); dtype F16, BF16 or F32 (all four equal).
+ * bias         : [Hh, N, N], strides (h, i, j), dtype F32/F16/BF16.
+ * mask         : [mask_batch, N, N] or NULL; strides (m, i, j); mask_batch
+ *                must divide B (1 broadcasts, B is per window, nW repeats
+ *                the per-window masks over an outer batch).
+ * boundary     : [B] uint8 or NULL.  When NULL and mask != NULL every window
+ *                reads its mask; a zero flag skips the mask for that window.
+ * scale        : softmax scale; q is multiplied by it in fp32 and rounded
+ *                back to the input type before the product.
+ * workspace    : device buffer of at least
+ *                crumpet_fused_swin_attention_workspace_size(Hh, N) bytes,
+ *                16-byte aligned.  It holds the padded fp32 copy of the bias
+ *                built at the start of the call.
+ *
+ * Supported: Dh in {16, 32, 64}, 1 <= N <= 512.
+ *
+ * Replaces the Triton launch of `_fused_swin_attention_kernel`,
+ * torch-ext/crumpet/fused_attention.py:48-146 (wrapper :149-226).  The
+ * reference had no dispatcher op for attention; the torch binding adds
+ * `crumpet_ops::fused_swin_attention`.
+ */
+int crumpet_fused_swin_attention(void* out, const int64_t out_strides[4],
+                                 const void* q, const int64_t q_strides[4],
+                                 const void* k, const int64_t k_strides[4],
+                                 const void* v, const int64_t v_strides[4],
+                                 int32_t dtype,
+                                 int64_t B, int64_t Hh, int64_t N, int64_t Dh,
+                                 const void* bias, int32_t bias_dtype,
+                                 const int64_t bias_strides[3],
+                                 const void* mask, int32_t mask_dtype, int64_t mask_batch,
+                                 const int64_t mask_strides[3],
+                                 const uint8_t* boundary,
+                                 float scale,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/* Bytes of workspace crumpet_fused_swin_attention needs for Hh heads and N tokens. */
+size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* CRUMPET_HIP_H_ */

@@ -1,0 +1,188 @@
+"""Parity of the HIP fused window attention with the fp32 oracle formula
+softmax(q*scale @ k^T + bias + [boundary]*mask) @ v (oracle/oracle.py).
+
+Tolerances (max-abs vs fp32 on the same low-precision inputs): 2e-3 fp16,
+1e-2 bf16, 1e-4 fp32.  The reference has no attention test; the cases here
+cover its wrapper semantics (torch-ext/crumpet/fused_attention.py:149-226):
+mask None / broadcast [1,N,N] / per-window [B,N,N], boundary flags, default
+scale, strided q/k/v, and the BASELINE shapes (N=343 with 3/6/12/24 heads,
+the MONAI N=216 stage-3 case).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from crumpet_amd.fused_attention import fused_swin_attention, fused_swin_attention_windows
+from helpers import TOL, bias_from_table, boundary_flags, seeded, trunc_normal_table
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(B, H, N, D, dtype, seed):
+    q = seeded((B, H, N, D), dtype, seed)
+    k = seeded((B, H, N, D), dtype, seed + 1)
+    v = seeded((B, H, N, D), dtype, seed + 2)
+    return q, k, v
+
+
+def _ws_for(N):
+    for w in range(1, 9):
+        if w ** 3 == N:
+            return (w, w, w)
+    raise ValueError(N)
+
+
+def _bias(H, N, dtype, seed):
+    ws = _ws_for(N)
+    rows = (2 * ws[0] - 1) * (2 * ws[1] - 1) * (2 * ws[2] - 1)
+    return bias_from_table(trunc_normal_table(rows, H, seed), ws).to(dtype)
+
+
+def _f32(t):
+    return t.float().numpy()
+
+
+def _compare(out, ref, dtype, what=""):
+    err = np.abs(out.float().cpu().numpy() - ref).max()
+    print(f"{what} max-abs {err:.3e} (tol {TOL[dtype]})", flush=True)
+    assert np.isfinite(out.float().cpu().numpy()).all()
+    assert err <= TOL[dtype], f"{what}: max-abs {err} > {TOL[dtype]}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_shifted_mask_per_window_with_boundary(oracle, dev, dtype):
+    D = 14
+    ws, ss = (7, 7, 7), (3, 3, 3)
+    B, H, N, Dh = 8 * 2, 3, 343, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 100)
+    bias = _bias(H, N, dtype, 101)
+    m8 = torch.from_numpy(oracle.attn_mask(D, D, D, ws, ss, "float32")).to(dtype)
+    mask = m8.repeat(2, 1, 1)
+    bnd = boundary_flags(D, D, D, ws, ss, outer=2)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), bnd.numpy(), scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), bnd.to(dev), scale=0.25)
+    assert out.dtype == dtype and out.shape == q.shape
+    _compare(out, ref, dtype, f"shifted {dtype}")
+    # boundary=None: every window reads its mask; same answer here
+    out2 = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), None, scale=0.25)
+    _compare(out2, ref, dtype, "boundary None")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_no_mask_and_default_scale(oracle, dev, dtype):
+    B, H, N, Dh = 5, 6, 343, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 200)
+    bias = _bias(H, N, dtype, 201)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=None)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), None)
+    _compare(out, ref, dtype, "no mask")
+
+
+def test_boundary_flag_skips_mask(oracle, dev):
+    dtype = torch.float16
+    B, H, N, Dh = 4, 2, 64, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 300)
+    bias = _bias(H, N, dtype, 301)
+    g = torch.Generator().manual_seed(302)
+    mask = torch.where(torch.rand((B, N, N), generator=g) < 0.4, -100.0, 0.0).to(dtype)
+    bnd = torch.tensor([1, 0, 0, 1], dtype=torch.uint8)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), bnd.numpy(), scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev),
+                               bnd.to(dev).bool(), scale=0.25)
+    _compare(out, ref, dtype, "boundary flags")
+
+
+def test_broadcast_mask_and_fp32_mask(oracle, dev):
+    dtype = torch.float16
+    B, H, N, Dh = 6, 3, 125, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 400)
+    bias = _bias(H, N, torch.float32, 401)  # fp32 bias with fp16 q/k/v
+    g = torch.Generator().manual_seed(402)
+    mask = torch.randn((1, N, N), generator=g) * 3.0  # arbitrary fp32 values
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), mask.numpy(), None, scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), None, scale=0.25)
+    _compare(out, ref, dtype, "broadcast fp32 mask")
+
+
+def test_mask_repeat_by_window_index(oracle, dev):
+    """mask [nW, N, N] with B = outer * nW: window b reads mask[b % nW]."""
+    dtype = torch.bfloat16
+    D, ws, ss = 14, (7, 7, 7), (3, 3, 3)
+    B, H, N, Dh = 8 * 3, 3, 343, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 500)
+    bias = _bias(H, N, dtype, 501)
+    m8 = torch.from_numpy(oracle.attn_mask(D, D, D, ws, ss, "float32")).to(dtype)
+    bnd = boundary_flags(D, D, D, ws, ss, outer=3)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(m8), bnd.numpy(), scale=0.25)
+    out = torch.empty_like(q, device=dev)
+    fused_swin_attention_windows(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), m8.to(dev), bnd.to(dev), 0.25, out)
+    _compare(out, ref, dtype, "mask mod nW")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_strided_qkv_views_and_strided_out(oracle, dev, dtype):
+    """q, k, v as views of a [b, n, 3, H, d] qkv buffer (monai_patch.py:153-154) and
+    the output written straight into a [b, n, H*d] buffer."""
+    b, n, H, Dh = 8, 343, 3, 16
+    qkv = seeded((b, n, 3 * H * Dh), dtype, 600)
+    t = qkv.reshape(b, n, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    q, k, v = t[0], t[1], t[2]
+    bias = _bias(H, n, dtype, 601)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=0.25)
+    td = qkv.to(dev).reshape(b, n, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    out_bnc = torch.empty((b, n, H * Dh), dtype=dtype, device=dev)
+    out = out_bnc.view(b, n, H, Dh).permute(0, 2, 1, 3)
+    fused_swin_attention(td[0], td[1], td[2], bias.to(dev), None, scale=0.25, out=out)
+    _compare(out, ref, dtype, "strided")
+    assert torch.equal(out_bnc.view(b, n, H, Dh).permute(0, 2, 1, 3).cpu(), out.cpu())
+
+
+@pytest.mark.parametrize("N", [8, 27, 64, 125, 216, 512])
+def test_window_volumes(oracle, dev, N):
+    dtype = torch.float16
+    B, H, Dh = 4, 2, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 700 + N)
+    bias = _bias(H, N, dtype, 701)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), None, scale=0.25)
+    _compare(out, ref, dtype, f"N={N}")
+
+
+def test_non_unit_d_stride(oracle, dev):
+    dtype = torch.float16
+    B, H, N, Dh = 3, 2, 64, 16
+    big = seeded((B, H, N, Dh * 2), dtype, 800)
+    q = big[..., ::2]
+    k = seeded((B, H, N, Dh), dtype, 801)
+    v = seeded((B, H, N, Dh), dtype, 802)
+    bias = _bias(H, N, dtype, 803)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=0.25)
+    out = fused_swin_attention(big.to(dev)[..., ::2], k.to(dev), v.to(dev), bias.to(dev), None, scale=0.25)
+    _compare(out, ref, dtype, "non-unit d stride")
+
+
+def test_config3_stage0_sampled(oracle, dev):
+    """qkv [1372, 343, 144] fp16, table [2197, 3] trunc-normal 0.02,
+    49^3 shifted mask tiled over sw-batch 4, scale 0.25.  The oracle checks a
+    sample of windows (all boundary types included); every output is finite."""
+    dtype = torch.float16
+    D, ws, ss = 49, (7, 7, 7), (3, 3, 3)
+    B, H, N, Dh = 1372, 3, 343, 16
+    qkv = seeded((B, N, 3 * H * Dh), dtype, 900)
+    table = trunc_normal_table(2197, H, 901)
+    bias = bias_from_table(table, ws).to(dtype)
+    m = torch.from_numpy(oracle.attn_mask(D, D, D, ws, ss, "float32")).to(dtype)
+    mask = m.repeat(4, 1, 1)
+    bnd = boundary_flags(D, D, D, ws, ss, outer=4)
+    td = qkv.to(dev).reshape(B, N, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    out = fused_swin_attention(td[0].contiguous(), td[1].contiguous(), td[2].contiguous(), bias.to(dev),
+                               mask.to(dev), bnd.to(dev), scale=0.25)
+    assert torch.isfinite(out).all()
+    sample = np.unique(np.concatenate([np.arange(0, B, 37), np.arange(335, 343), np.arange(1364, 1372)]))
+    t = qkv[sample].reshape(len(sample), N, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), _f32(mask[sample]),
+                           bnd.numpy()[sample], scale=0.25)
+    _compare(out[torch.from_numpy(sample).to(dev)], ref, dtype, "config3 sample")

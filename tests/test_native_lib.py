@@ -1,0 +1,107 @@
+"""CPU checks of the native boundary: the C-ABI library loads and exports
+every symbol include/crumpet_hip.h declares, the torch binding registers the
+crumpet_ops schemas, and the host-side argument checks of the C ABI return
+their error codes without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from helpers import c_abi
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    text = (ROOT / "include" / "crumpet_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(crumpet_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    from crumpet_amd import _native
+
+    declared = _declared_symbols()
+    assert len(declared) >= 10
+    lib = ctypes.CDLL(str(_native.HIP_LIB))
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.C_ABI_SYMBOLS)
+
+
+def test_version_and_status_strings():
+    lib = c_abi()
+    assert lib.crumpet_version() == b"0.1.0"
+    assert lib.crumpet_status_string(0) == b"CRUMPET_OK"
+    assert lib.crumpet_status_string(1) == b"CRUMPET_ERR_INVALID_ARGUMENT"
+    assert lib.crumpet_status_string(2) == b"CRUMPET_ERR_UNSUPPORTED"
+    assert lib.crumpet_status_string(3) == b"CRUMPET_ERR_HIP"
+
+
+def test_workspace_size_closed_form():
+    lib = c_abi()
+    assert lib.crumpet_fused_swin_attention_workspace_size(3, 343) == 3 * 352 * 352 * 4
+    assert lib.crumpet_fused_swin_attention_workspace_size(24, 216) == 24 * 224 * 224 * 4
+    assert lib.crumpet_fused_swin_attention_workspace_size(0, 343) == 0
+
+
+def test_host_argument_checks_need_no_gpu():
+    """Invalid arguments are rejected before any HIP call."""
+    lib = c_abi()
+    fake = ctypes.c_void_p(16)
+    st = lib.crumpet_shift_partition_3d(fake, fake, 1, 15, 14, 14, 4, 2, 7, 7, 7, 3, 3, 3, None)
+    assert st == 1 and b"divisible" in lib.crumpet_last_error()
+    st = lib.crumpet_unshift_unpartition_3d(fake, fake, 1, 14, 14, 14, 4, 2, 7, 7, 7, 7, 0, 0, None)
+    assert st == 1 and b"shift" in lib.crumpet_last_error()
+    st = lib.crumpet_shift_partition_3d(fake, fake, 1, 14, 14, 14, 4, 3, 7, 7, 7, 3, 3, 3, None)
+    assert st == 1 and b"elem_size" in lib.crumpet_last_error()
+    st = lib.crumpet_compute_attn_mask_3d(fake, 1, 11, 11, 11, 11, 11, 11, 5, 5, 5, None)
+    assert st == 2 and b"1024" in lib.crumpet_last_error()
+    st = lib.crumpet_compute_attn_mask_3d(fake, 7, 14, 14, 14, 7, 7, 7, 3, 3, 3, None)
+    assert st == 1
+    # zero-size work is a successful no-op
+    assert lib.crumpet_shift_partition_3d(None, None, 0, 14, 14, 14, 4, 2, 7, 7, 7, 3, 3, 3, None) == 0
+
+
+def test_attention_argument_checks_need_no_gpu():
+    lib = c_abi()
+    s4 = (ctypes.c_int64 * 4)(1, 1, 1, 1)
+    s3 = (ctypes.c_int64 * 3)(1, 1, 1)
+    fake = ctypes.c_void_p(256)
+
+    def call(dtype=1, B=2, H=3, N=343, Dh=16, mask=None, mb=1, ws=fake, wsb=1 << 30):
+        return lib.crumpet_fused_swin_attention(
+            fake, s4, fake, s4, fake, s4, fake, s4, dtype, B, H, N, Dh, fake, 1, s3,
+            mask, 1, mb, s3, None, ctypes.c_float(0.25), ws, wsb, None)
+
+    assert call(Dh=8) == 2
+    assert call(N=600) == 2
+    assert call(dtype=5) == 1
+    assert call(mask=fake, mb=3) == 1  # mask batch must divide B
+    assert call(wsb=16) == 1  # workspace too small
+    assert call(B=0) == 0
+
+
+def test_dispatcher_schemas_match_reference():
+    import crumpet_amd  # noqa: F401  (loads the binding)
+
+    ops = torch.ops.crumpet_ops
+    expect = {
+        "compute_attn_mask_3d": "(Tensor(a0!) output, int D, int H, int W, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        "fused_shift_partition_3d": "(Tensor(a0!) output, Tensor x, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        "fused_shift_partition_3d_backward": "(Tensor(a0!) grad_x, Tensor grad_windows, int B, int D, int H, int W, int C, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        "fused_unshift_unpartition_3d": "(Tensor(a0!) output, Tensor windows, int B, int D, int H, int W, int C, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        "fused_unshift_unpartition_3d_backward": "(Tensor(a0!) grad_windows, Tensor grad_x, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+    }
+    for name, sig in expect.items():
+        schema = str(getattr(ops, name).default._schema)
+        norm = re.sub(r"\(\$?a?\d+! -> \)", "(a0!)", schema)
+        norm = re.sub(r"Tensor\([^)]*!\)", "Tensor(a0!)", norm)
+        assert norm == f"crumpet_ops::{name}{sig}", schema
+        assert torch.Tag.pt2_compliant_tag in getattr(ops, name).default.tags
+        assert torch.Tag.needs_fixed_stride_order in getattr(ops, name).default.tags
