@@ -99,7 +99,7 @@ def build_binding(verbose: bool = False) -> Path:
         str(CSRC / "torch_binding.cpp"),
         "-o", str(tmp),
         f"-L{PKG}", "-lcrumpet_hip",
-        f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch_cpu",
+        f"-L{tlib}", "-lc10", "-lc10_hip", "-ltorch_cpu", "-ltorch_hip",
         "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tlib}",
     ]
     _run(cmd, verbose)

@@ -4,13 +4,14 @@
 // (torch-ext/torch_binding.cpp:10-31), plus `fused_swin_attention`, which
 // the reference launched from Python through Triton.  Every impl checks
 // shapes, dtypes and devices (so no launch can index outside its tensors),
-// takes the current HIP stream of the tensor's device and forwards to the
+// takes the current HIP stream of the tensor's device (ROCm torch tags HIP
+// devices as "cuda", hence the masquerading guard/stream helpers) and forwards to the
 // C ABI of libcrumpet_hip.so (include/crumpet_hip.h).  A non-OK status
 // becomes a RuntimeError carrying crumpet_last_error().
 #include <ATen/core/Tensor.h>
 #include <ATen/ops/empty.h>
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 #include <torch/library.h>
 
 #include "crumpet_hip.h"
@@ -23,7 +24,8 @@ const std::vector<at::Tag> kCrumpetOpTags = {
 };
 
 void* stream_of(const at::Tensor& t) {
-    return static_cast<void*>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
+    return static_cast<void*>(
+        c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(t.device().index()).stream());
 }
 
 void check_status(int status) {
@@ -51,7 +53,7 @@ int32_t dtype_code(at::ScalarType t) {
 void compute_attn_mask_3d(at::Tensor& output, int64_t D, int64_t H, int64_t W, int64_t ws_d,
                           int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w) {
     TORCH_CHECK(output.is_cuda(), "compute_attn_mask_3d: output must be on a HIP device");
-    const c10::hip::HIPGuard guard(output.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(output.device());
     if (output.numel() == 0) return;
     const int32_t dt = dtype_code(output.scalar_type());
     TORCH_CHECK(dt >= 0, "compute_attn_mask_3d: output dtype must be float32, float16 or bfloat16");
@@ -70,7 +72,7 @@ void fused_shift_partition_3d(at::Tensor& output, const at::Tensor& x, int64_t w
                               int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w) {
     TORCH_CHECK(x.dim() == 5, "fused_shift_partition_3d: x must have shape [B, D, H, W, C]");
     check_device_pair(output, x, "fused_shift_partition_3d");
-    const c10::hip::HIPGuard guard(x.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
     if (output.numel() == 0) return;
     check_status(crumpet_shift_partition_3d(output.data_ptr(), x.data_ptr(), x.size(0), x.size(1),
                                             x.size(2), x.size(3), x.size(4), x.element_size(),
@@ -82,7 +84,7 @@ void fused_unshift_unpartition_3d(at::Tensor& output, const at::Tensor& windows,
                                   int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h,
                                   int64_t ss_w) {
     check_device_pair(output, windows, "fused_unshift_unpartition_3d");
-    const c10::hip::HIPGuard guard(windows.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(windows.device());
     if (output.numel() == 0) return;
     TORCH_CHECK(output.numel() == B * D * H * W * C,
                 "fused_unshift_unpartition_3d: output must hold B*D*H*W*C elements");
@@ -96,7 +98,7 @@ void fused_shift_partition_3d_backward(at::Tensor& grad_x, const at::Tensor& gra
                                        int64_t ws_d, int64_t ws_h, int64_t ws_w, int64_t ss_d,
                                        int64_t ss_h, int64_t ss_w) {
     check_device_pair(grad_x, grad_windows, "fused_shift_partition_3d_backward");
-    const c10::hip::HIPGuard guard(grad_windows.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(grad_windows.device());
     if (grad_x.numel() == 0) return;
     TORCH_CHECK(grad_x.numel() == B * D * H * W * C,
                 "fused_shift_partition_3d_backward: grad_x must hold B*D*H*W*C elements");
@@ -111,7 +113,7 @@ void fused_unshift_unpartition_3d_backward(at::Tensor& grad_windows, const at::T
     TORCH_CHECK(grad_x.dim() == 5,
                 "fused_unshift_unpartition_3d_backward: grad_x must have shape [B, D, H, W, C]");
     check_device_pair(grad_windows, grad_x, "fused_unshift_unpartition_3d_backward");
-    const c10::hip::HIPGuard guard(grad_x.device());
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(grad_x.device());
     if (grad_windows.numel() == 0) return;
     check_status(crumpet_unshift_unpartition_3d_backward(
         grad_windows.data_ptr(), grad_x.data_ptr(), grad_x.size(0), grad_x.size(1),
@@ -169,7 +171,7 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
                     ": boundary must be a contiguous [B] tensor");
         bptr = static_cast<const uint8_t*>(bd.data_ptr());
     }
-    const c10::hip::HIPGuard guard(dev);
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
     if (out.numel() == 0) return;
     const size_t ws_bytes = crumpet_fused_swin_attention_workspace_size(Hh, N);
     at::Tensor ws = at::empty({static_cast<int64_t>((ws_bytes + 15) / 16) * 4},
