@@ -32,13 +32,17 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["api.hip", "partition.hip", "attn_mask.hip", "attention.hip"]
+HIP_SOURCES = [
+    "api.hip", "partition.hip", "attn_mask.hip", "attention.hip",
+    "attention_f16.hip", "attention_bf16.hip", "attention_f32.hip",
+]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
     "-std=c++17",
     "-fPIC",
+    "-fvisibility=hidden",
     # packed fp32 VALU ops stay disabled on these boxes
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",

@@ -1,0 +1,10 @@
+// bf16 instantiations of the fused window attention kernel (attention_kernel.h).
+#include "attention_kernel.h"
+
+namespace crumpet {
+namespace attn {
+
+void launch_bf16(const Params& p, int NT, int kmask, hipStream_t s) { launch<__bf16>(p, NT, kmask, s); }
+
+}  // namespace attn
+}  // namespace crumpet

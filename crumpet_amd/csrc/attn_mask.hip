@@ -2,8 +2,9 @@
 //
 // The mask [nW, vol, vol] is written as one flat array of 16-byte vectors
 // (8 fp16/bf16 or 4 fp32 elements), so every store is a full, aligned,
-// coalesced 16-byte non-temporal store, whatever the odd window volume
-// (vol^2 = 117649 at ws=7 leaves the per-window blocks only 2-byte aligned).
+// coalesced 16-byte store, whatever the odd window volume (vol^2 = 117649 at
+// ws=7 leaves the per-window blocks only 2-byte aligned).  Plain stores beat
+// non-temporal ones for this pure write stream on MI355X.
 //
 // Which value an element holds follows from two 3-bit codes:
 //   cls[loc]  : for each axis, whether the local coordinate lies at or past
@@ -18,8 +19,12 @@
 // not the last along an axis every coordinate lies in region 0; in the last
 // window the coordinate x = dim - ws + loc is in region 1 when loc < ws - ss
 // and in region 2 otherwise (region(x) definition: cuda/attn_mask_3d.cu:42-50,
-// torch-ext/crumpet/reference.py:80-98).  Interior windows (split == 0) take
-// a zero-store fast path with no table reads.
+// torch-ext/crumpet/reference.py:80-98).
+//
+// Workgroups whose range touches only interior windows (split == 0, 80% of
+// the output at 98^3) skip the table and store zeros.  In boundary ranges a
+// vector that straddles two mask rows picks the next row's class and split
+// with branch-free selects, so no lane forces its wave down a slow path.
 #include <hip/hip_runtime.h>
 
 #include "crumpet_common.h"
@@ -30,7 +35,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxVolume = 1024;  // same limit as cuda/attn_mask_3d.cu:143
-constexpr int kVecPerThread = 4;
+constexpr int kVecPerThread = 2;
 
 struct MaskGeom {
     uint32_t total_elems;  // elements written by this launch (< 2^31)
@@ -55,83 +60,91 @@ __device__ __forceinline__ uint32_t split_of(uint32_t win, const MaskGeom& g) {
 // kEsize: 2 (fp16/bf16) or 4 (fp32); kNeg: bit pattern of -100 in that type.
 template <int kEsize, uint32_t kNeg>
 __global__ void __launch_bounds__(kThreads)
-attn_mask_kernel(u32x4* __restrict__ out, const MaskGeom g, const uint32_t chunks,
-                 const uint32_t launched) {
-    constexpr uint32_t kEpv = 16 / kEsize;  // elements per vector
+attn_mask_kernel(u32x4* __restrict__ out, const MaskGeom g) {
+    constexpr uint32_t kEpv = 16 / kEsize;  // elements per 16-byte vector
+    constexpr uint32_t kSpan = kThreads * kVecPerThread * kEpv;  // elements per workgroup
     __shared__ uint8_t cls[kMaxVolume];
 
-    uint32_t chunk;
-    const bool active = xcd_chunk(blockIdx.x, launched, chunks, chunk);
-    if (!active) return;  // whole workgroup exits together
-
-    for (uint32_t loc = threadIdx.x; loc < g.vol; loc += kThreads) {
-        uint32_t lt, lw, ld, lh;
-        g.f_wsw.divmod(loc, lt, lw);
-        g.f_wsh.divmod(lt, ld, lh);
-        cls[loc] = static_cast<uint8_t>(((ld >= g.ws_d - g.ss_d) ? 4 : 0) |
-                                        ((lh >= g.ws_h - g.ss_h) ? 2 : 0) |
-                                        ((lw >= g.ws_w - g.ss_w) ? 1 : 0));
+    const uint32_t e_first = blockIdx.x * kSpan;
+    const uint32_t e_last = min(g.total_elems, e_first + kSpan) - 1;
+    // Workgroup-uniform: does this range touch a window split by the shift?
+    // (A range that spans more than two windows only happens for tiny windows.)
+    uint32_t w_first, w_last, r0;
+    g.f_vol.divmod(e_first, w_first, r0);
+    w_first = g.f_vol.div(w_first);
+    g.f_vol.divmod(e_last, w_last, r0);
+    w_last = g.f_vol.div(w_last);
+    const bool boundary = (w_last > w_first + 1) || split_of(g.win0 + w_first, g) != 0 ||
+                          split_of(g.win0 + w_last, g) != 0;
+    if (boundary) {
+        for (uint32_t loc = threadIdx.x; loc < g.vol; loc += kThreads) {
+            uint32_t lt, lw, ld, lh;
+            g.f_wsw.divmod(loc, lt, lw);
+            g.f_wsh.divmod(lt, ld, lh);
+            cls[loc] = static_cast<uint8_t>(((ld >= g.ws_d - g.ss_d) ? 4 : 0) |
+                                            ((lh >= g.ws_h - g.ss_h) ? 2 : 0) |
+                                            ((lw >= g.ws_w - g.ss_w) ? 1 : 0));
+        }
+        __syncthreads();
     }
-    __syncthreads();
 
     const uint32_t nvec = (g.total_elems + kEpv - 1) / kEpv;
-    const uint32_t base = chunk * (kThreads * kVecPerThread) + threadIdx.x;
 #pragma unroll
     for (int u = 0; u < kVecPerThread; ++u) {
-        const uint32_t vi = base + u * kThreads;
+        const uint32_t vi = blockIdx.x * (kThreads * kVecPerThread) + u * kThreads + threadIdx.x;
         if (vi >= nvec) break;
         const uint32_t e0 = vi * kEpv;
-        uint32_t row, j0, wl, i;
-        g.f_vol.divmod(e0, row, j0);
-        g.f_vol.divmod(row, wl, i);
-        const uint32_t sm = split_of(g.win0 + wl, g);
-        u32x4 v = {0u, 0u, 0u, 0u};
-        if (j0 + kEpv <= g.vol && e0 + kEpv <= g.total_elems) {
-            // the whole vector lies in one mask row
-            if (sm != 0) {
-                const uint32_t ci = cls[i];
-                uint32_t bits[kEpv];
+        uint32_t bits[kEpv];
 #pragma unroll
-                for (uint32_t k = 0; k < kEpv; ++k)
-                    bits[k] = ((cls[j0 + k] ^ ci) & sm) ? kNeg : 0u;
+        for (uint32_t k = 0; k < kEpv; ++k) bits[k] = 0u;
+        if (boundary) {
+            if (g.vol >= kEpv) {
+                // at most one row wrap inside the vector
+                uint32_t row, j0, w, i;
+                g.f_vol.divmod(e0, row, j0);
+                g.f_vol.divmod(row, w, i);
+                const uint32_t sm = split_of(g.win0 + w, g);
+                const bool last_row = (i + 1 == g.vol);
+                const uint32_t i1 = last_row ? 0u : i + 1;
+                const uint32_t sm1 = last_row ? split_of(g.win0 + w + 1, g) : sm;
+                const bool straddle = j0 + kEpv > g.vol;
+                if ((sm | (straddle ? sm1 : 0u)) != 0u) {
+                    const uint32_t c0 = cls[i];
+                    const uint32_t c1 = cls[i1];
 #pragma unroll
-                for (uint32_t m = 0; m < 4; ++m) {
-                    if (kEsize == 2)
-                        v[m] = bits[2 * m] | (bits[2 * m + 1] << 16);
-                    else
-                        v[m] = bits[m];
+                    for (uint32_t k = 0; k < kEpv; ++k) {
+                        const uint32_t j = j0 + k;
+                        const bool wrap = j >= g.vol;
+                        const uint32_t jj = wrap ? j - g.vol : j;
+                        const uint32_t ci = wrap ? c1 : c0;
+                        const uint32_t s = wrap ? sm1 : sm;
+                        bits[k] = ((cls[jj] ^ ci) & s) ? kNeg : 0u;
+                    }
                 }
-            }
-            __builtin_nontemporal_store(v, out + vi);
-        } else {
-            // vector crosses a row (or window) boundary, or is the tail
-            uint32_t bits[kEpv];
-#pragma unroll
-            for (uint32_t k = 0; k < kEpv; ++k) {
-                const uint32_t e = e0 + k;
-                uint32_t r, j, w, ii;
-                g.f_vol.divmod(e, r, j);
-                g.f_vol.divmod(r, w, ii);
-                const uint32_t s = split_of(g.win0 + w, g);
-                bits[k] = (e < g.total_elems && ((cls[j] ^ cls[ii]) & s)) ? kNeg : 0u;
-            }
-            if (e0 + kEpv <= g.total_elems) {
-#pragma unroll
-                for (uint32_t m = 0; m < 4; ++m) {
-                    if (kEsize == 2)
-                        v[m] = bits[2 * m] | (bits[2 * m + 1] << 16);
-                    else
-                        v[m] = bits[m];
-                }
-                __builtin_nontemporal_store(v, out + vi);
             } else {
-                // partial tail vector: scalar stores of the elements in range
-                for (uint32_t k = 0; k < kEpv && e0 + k < g.total_elems; ++k) {
-                    if (kEsize == 2)
-                        reinterpret_cast<uint16_t*>(out)[e0 + k] = static_cast<uint16_t>(bits[k]);
-                    else
-                        reinterpret_cast<uint32_t*>(out)[e0 + k] = bits[k];
+                // tiny windows: every element decodes its own (window, row, column)
+#pragma unroll
+                for (uint32_t k = 0; k < kEpv; ++k) {
+                    uint32_t r, j, w, ii;
+                    g.f_vol.divmod(e0 + k, r, j);
+                    g.f_vol.divmod(r, w, ii);
+                    bits[k] = ((cls[j] ^ cls[ii]) & split_of(g.win0 + w, g)) ? kNeg : 0u;
                 }
+            }
+        }
+        if (e0 + kEpv <= g.total_elems) {
+            u32x4 v;
+#pragma unroll
+            for (uint32_t m = 0; m < 4; ++m)
+                v[m] = (kEsize == 2) ? (bits[2 * m] | (bits[2 * m + 1] << 16)) : bits[m];
+            out[vi] = v;
+        } else {
+            // partial tail vector: scalar stores of the elements in range
+            for (uint32_t k = 0; k < kEpv && e0 + k < g.total_elems; ++k) {
+                if (kEsize == 2)
+                    reinterpret_cast<uint16_t*>(out)[e0 + k] = static_cast<uint16_t>(bits[k]);
+                else
+                    reinterpret_cast<uint32_t*>(out)[e0 + k] = bits[k];
             }
         }
     }
@@ -202,19 +215,18 @@ extern "C" int crumpet_compute_attn_mask_3d(void* out, int32_t dtype, int64_t D,
         g.total_elems = static_cast<uint32_t>(nwin * pair);
         const int64_t epv = 16 / esize;
         const int64_t nvec = (nwin * pair + epv - 1) / epv;
-        const uint32_t chunks =
+        const uint32_t blocks =
             static_cast<uint32_t>((nvec + kThreads * kVecPerThread - 1) / (kThreads * kVecPerThread));
-        const uint32_t launched = xcd_launch_count(chunks);
         u32x4* dst = reinterpret_cast<u32x4*>(base + w0 * pair * esize);
         if (esize == 4)
-            hipLaunchKernelGGL((attn_mask_kernel<4, 0xC2C80000u>), dim3(launched), dim3(kThreads),
-                               0, s, dst, g, chunks, launched);
+            hipLaunchKernelGGL((attn_mask_kernel<4, 0xC2C80000u>), dim3(blocks), dim3(kThreads), 0,
+                               s, dst, g);
         else if (neg == 0xD640u)
-            hipLaunchKernelGGL((attn_mask_kernel<2, 0xD640u>), dim3(launched), dim3(kThreads), 0,
-                               s, dst, g, chunks, launched);
+            hipLaunchKernelGGL((attn_mask_kernel<2, 0xD640u>), dim3(blocks), dim3(kThreads), 0, s,
+                               dst, g);
         else
-            hipLaunchKernelGGL((attn_mask_kernel<2, 0xC2C8u>), dim3(launched), dim3(kThreads), 0,
-                               s, dst, g, chunks, launched);
+            hipLaunchKernelGGL((attn_mask_kernel<2, 0xC2C8u>), dim3(blocks), dim3(kThreads), 0, s,
+                               dst, g);
         const int st = check_launch(what);
         if (st != CRUMPET_OK) return st;
     }

@@ -147,8 +147,10 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
     int32_t mdt = 0;
     int64_t mbatch = 1;
     int64_t ms[3] = {0, 0, 0};
+    at::Tensor mask_t;
     if (mask.has_value()) {
-        const at::Tensor& m = *mask;
+        mask_t = mask->stride(2) == 1 ? *mask : mask->contiguous();
+        const at::Tensor& m = mask_t;
         TORCH_CHECK(m.device() == dev, what, ": mask must be on the same device");
         TORCH_CHECK(m.dim() == 3 && m.size(1) == N && m.size(2) == N, what,
                     ": mask must have shape [M, N, N]");

@@ -23,6 +23,14 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* Only these entry points are exported; everything else in the library is
+ * built with hidden visibility. */
+#if defined(__GNUC__)
+#define CRUMPET_API __attribute__((visibility("default")))
+#else
+#define CRUMPET_API
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -44,13 +52,13 @@ enum crumpet_dtype {
 };
 
 /* Library version, e.g. "0.1.0". */
-const char* crumpet_version(void);
+CRUMPET_API const char* crumpet_version(void);
 
 /* Message describing the last non-OK status returned on this thread. */
-const char* crumpet_last_error(void);
+CRUMPET_API const char* crumpet_last_error(void);
 
 /* Static name of a status code. */
-const char* crumpet_status_string(int status);
+CRUMPET_API const char* crumpet_status_string(int status);
 
 /*
  * Fused cyclic shift (torch.roll by -shift over D, H, W) plus 3D window
@@ -70,7 +78,7 @@ const char* crumpet_status_string(int status);
  * torch-ext/torch_binding.cpp:19-21, host entry
  * cuda/shift_partition_3d.cu:318-347.
  */
-int crumpet_shift_partition_3d(void* out, const void* x,
+CRUMPET_API int crumpet_shift_partition_3d(void* out, const void* x,
                                int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
                                int64_t elem_size,
                                int64_t ws_d, int64_t ws_h, int64_t ws_w,
@@ -88,7 +96,7 @@ int crumpet_shift_partition_3d(void* out, const void* x,
  * int B, int D, int H, int W, int C, ...)`, torch-ext/torch_binding.cpp:26-28,
  * host entry cuda/unshift_unpartition_3d.cu:284-318.
  */
-int crumpet_unshift_unpartition_3d(void* out, const void* windows,
+CRUMPET_API int crumpet_unshift_unpartition_3d(void* out, const void* windows,
                                    int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
                                    int64_t elem_size,
                                    int64_t ws_d, int64_t ws_h, int64_t ws_w,
@@ -103,7 +111,7 @@ int crumpet_unshift_unpartition_3d(void* out, const void* windows,
  * Replaces op `fused_shift_partition_3d_backward`, torch-ext/torch_binding.cpp:22-24,
  * host entry cuda/unshift_unpartition_3d.cu:320-348.
  */
-int crumpet_shift_partition_3d_backward(void* grad_x, const void* grad_windows,
+CRUMPET_API int crumpet_shift_partition_3d_backward(void* grad_x, const void* grad_windows,
                                         int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
                                         int64_t elem_size,
                                         int64_t ws_d, int64_t ws_h, int64_t ws_w,
@@ -117,7 +125,7 @@ int crumpet_shift_partition_3d_backward(void* grad_x, const void* grad_windows,
  * Replaces op `fused_unshift_unpartition_3d_backward`,
  * torch-ext/torch_binding.cpp:29-31, host entry cuda/shift_partition_3d.cu:349-367.
  */
-int crumpet_unshift_unpartition_3d_backward(void* grad_windows, const void* grad_x,
+CRUMPET_API int crumpet_unshift_unpartition_3d_backward(void* grad_windows, const void* grad_x,
                                             int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
                                             int64_t elem_size,
                                             int64_t ws_d, int64_t ws_h, int64_t ws_w,
@@ -139,7 +147,7 @@ int crumpet_unshift_unpartition_3d_backward(void* grad_windows, const void* grad
  * Replaces op `compute_attn_mask_3d(Tensor! output, int D, int H, int W, ...)`,
  * torch-ext/torch_binding.cpp:16-18, host entry cuda/attn_mask_3d.cu:127-168.
  */
-int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
+CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
                                  int64_t D, int64_t H, int64_t W,
                                  int64_t ws_d, int64_t ws_h, int64_t ws_w,
                                  int64_t ss_d, int64_t ss_h, int64_t ss_w,
@@ -154,7 +162,8 @@ int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  * q, k, v, out : [B, Hh, N, Dh] with arbitrary element strides (in elements,
  *                order b, h, n, d); dtype F16, BF16 or F32 (all four equal).
  * bias         : [Hh, N, N], strides (h, i, j), dtype F32/F16/BF16.
- * mask         : [mask_batch, N, N] or NULL; strides (m, i, j); mask_batch
+ * mask         : [mask_batch, N, N] or NULL; strides (m, i, j) with unit j
+ *                stride; mask_batch
  *                must divide B (1 broadcasts, B is per window, nW repeats
  *                the per-window masks over an outer batch).
  * boundary     : [B] uint8 or NULL.  When NULL and mask != NULL every window
@@ -166,14 +175,14 @@ int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  *                16-byte aligned.  It holds the padded fp32 copy of the bias
  *                built at the start of the call.
  *
- * Supported: Dh in {16, 32, 64}, 1 <= N <= 512.
+ * Supported: Dh = 16, 1 <= N <= 512.
  *
  * Replaces the Triton launch of `_fused_swin_attention_kernel`,
  * torch-ext/crumpet/fused_attention.py:48-146 (wrapper :149-226).  The
  * reference had no dispatcher op for attention; the torch binding adds
  * `crumpet_ops::fused_swin_attention`.
  */
-int crumpet_fused_swin_attention(void* out, const int64_t out_strides[4],
+CRUMPET_API int crumpet_fused_swin_attention(void* out, const int64_t out_strides[4],
                                  const void* q, const int64_t q_strides[4],
                                  const void* k, const int64_t k_strides[4],
                                  const void* v, const int64_t v_strides[4],
@@ -189,7 +198,7 @@ int crumpet_fused_swin_attention(void* out, const int64_t out_strides[4],
                                  void* stream);
 
 /* Bytes of workspace crumpet_fused_swin_attention needs for Hh heads and N tokens. */
-size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N);
+CRUMPET_API size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -34,6 +34,21 @@ def test_every_declared_symbol_is_exported():
     assert set(declared) == set(_native.C_ABI_SYMBOLS)
 
 
+def test_library_exports_only_the_c_abi():
+    """Internal C++ symbols and kernel stubs are hidden, so another library in
+    the process can neither interpose on them nor be interposed."""
+    import subprocess
+
+    from crumpet_amd import _native
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_native.HIP_LIB)],
+                         capture_output=True, text=True, check=True).stdout
+    names = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    ours = {n for n in names if not n.startswith(("_", "hip", "__"))}
+    assert ours == set(_declared_symbols())
+    assert not any("crumpet" in n for n in names - ours)
+
+
 def test_version_and_status_strings():
     lib = c_abi()
     assert lib.crumpet_version() == b"0.1.0"
