@@ -163,9 +163,18 @@ def bench_attention(args, dev):
         t = views[i % R]
         fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ovs[i % R])
 
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted
+
+    def attn_shifted(i):
+        t = views[i % R]
+        fused_swin_attention_shifted(t[0], t[1], t[2], bias, (C3["D"],) * 3, (7, 7, 7), (3, 3, 3),
+                                     0.25, ovs[i % R])
+
     _events_time(attn, args.warmup)
     t_attn = _events_time(attn, args.steps)
-    res = dict(t_attn=t_attn)
+    _events_time(attn_shifted, args.warmup)
+    t_shift = _events_time(attn_shifted, args.steps)
+    res = dict(t_attn=t_attn, t_shift=t_shift)
 
     # accuracy on a sample of windows vs fp32 torch (GPU) of the same inputs
     t = views[0]
@@ -308,6 +317,16 @@ def main():
             comp["eager_rocm_ms"] = round(a["t_eager"], 4)
             comp["speedup_vs_eager"] = round(a["t_eager"] / a["t_attn"], 2)
         components["attention"] = comp
+        tfl_s = C3_FLOPS / (a["t_shift"] * 1e-3) / 1e12
+        comp_s = {"ms": round(a["t_shift"], 5), "TFLOP_s": round(tfl_s, 2),
+                  "frac_mfma_f16": round(tfl_s / MFMA_F16_PEAK_TFLOPS, 4),
+                  "GB_s": round(C3_BYTES / (a["t_shift"] * 1e-3) / 1e9, 1),
+                  "frac_hbm": round(C3_BYTES / (a["t_shift"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "workload": "config 3 through fused_swin_attention_shifted (mask from the 49^3 "
+                              "geometry, never materialised)"}
+        if "t_eager" in a:
+            comp_s["speedup_vs_eager"] = round(a["t_eager"] / a["t_shift"], 2)
+        components["attention_shifted"] = comp_s
 
     line = {
         "metric": "partition/unpartition GB/s (% HBM peak); window-attn TFLOP/s; ms per 96³ fwd",

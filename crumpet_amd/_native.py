@@ -29,6 +29,8 @@ C_ABI_SYMBOLS = (
     "crumpet_compute_attn_mask_3d",
     "crumpet_fused_swin_attention",
     "crumpet_fused_swin_attention_workspace_size",
+    "crumpet_fused_swin_attention_shifted",
+    "crumpet_fused_swin_attention_shifted_workspace_size",
 )
 
 OP_NAMES = (
@@ -38,6 +40,7 @@ OP_NAMES = (
     "fused_unshift_unpartition_3d",
     "fused_unshift_unpartition_3d_backward",
     "fused_swin_attention",
+    "fused_swin_attention_shifted",
 )
 
 _hip = None

@@ -1,7 +1,8 @@
-// Host side of the fused window attention: argument checks, the padded
-// fp32 bias workspace, and dispatch to the per-dtype kernel instantiations
-// (attention_f16.hip, attention_bf16.hip, attention_f32.hip; the kernel
-// itself is in attention_kernel.h).
+// Host side of the fused window attention: argument checks, the fp32 bias
+// (+ shifted-window mask) tables in the workspace, the window-type table of
+// the region mode, the work decomposition, and dispatch to the per-dtype
+// kernel instantiations (attention_f16.hip, attention_bf16.hip,
+// attention_f32.hip; the kernel itself is in attention_kernel.h).
 //
 // Replaces the Triton launch of torch-ext/crumpet/fused_attention.py:149-226.
 #include <hip/hip_runtime.h>
@@ -16,27 +17,49 @@ namespace crumpet {
 namespace {
 
 constexpr int kPrepThreads = 256;
+// Workgroups a call aims for: each walks win_per_wg windows; ~4 per CU.
+constexpr int64_t kTargetWorkgroups = 1024;
 
-// Padded fp32 copy of the bias: ws[h][i][j] = bias[h][i][j] for i, j < N,
-// -inf in padded key columns, 0 in padded query rows of real keys.
+// Local-coordinate class of a window token for the shifted-window mask:
+// one bit per axis, set when the coordinate lies at or past ws - ss.
+struct RegionCls {
+    int32_t ws_d, ws_h, ws_w, ss_d, ss_h, ss_w;
+    __device__ __forceinline__ int cls(int loc) const {
+        const int lw = loc % ws_w;
+        const int t = loc / ws_w;
+        const int lh = t % ws_h;
+        const int ld = t / ws_h;
+        return ((ld >= ws_d - ss_d) ? 4 : 0) | ((lh >= ws_h - ss_h) ? 2 : 0) |
+               ((lw >= ws_w - ss_w) ? 1 : 0);
+    }
+};
+
+// tables[c][h][i][j] (c < ntables): bias[h][i][j], plus -100 where the
+// shifted-window mask of window type code c separates tokens i and j
+// (region mode only); -inf in padded key columns, 0 in padded query rows.
 template <typename TB>
 __global__ void __launch_bounds__(kPrepThreads)
-bias_prep_kernel(float* __restrict__ ws, const TB* __restrict__ bias, int64_t sh, int64_t si,
-                 int64_t sj, int32_t H, int32_t N, int32_t NP) {
-    const int64_t total = int64_t(H) * NP * NP;
+table_prep_kernel(float* __restrict__ ws, const TB* __restrict__ bias, int64_t sh, int64_t si,
+                  int64_t sj, int32_t H, int32_t N, int32_t NP, int32_t ntables, int32_t region,
+                  RegionCls rc) {
+    const int64_t total = int64_t(ntables) * H * NP * NP;
     for (int64_t idx = int64_t(blockIdx.x) * kPrepThreads + threadIdx.x; idx < total;
          idx += int64_t(gridDim.x) * kPrepThreads) {
         const int32_t j = static_cast<int32_t>(idx % NP);
-        const int64_t r = idx / NP;
+        int64_t r = idx / NP;
         const int32_t i = static_cast<int32_t>(r % NP);
-        const int32_t h = static_cast<int32_t>(r / NP);
+        r /= NP;
+        const int32_t h = static_cast<int32_t>(r % H);
+        const int32_t code = static_cast<int32_t>(r / H);
         float val;
-        if (j >= N)
+        if (j >= N) {
             val = -INFINITY;
-        else if (i >= N)
+        } else if (i >= N) {
             val = 0.0f;
-        else
+        } else {
             val = static_cast<float>(bias[h * sh + i * si + j * sj]);
+            if (region && ((rc.cls(i) ^ rc.cls(j)) & code)) val += -100.0f;
+        }
         ws[idx] = val;
     }
 }
@@ -50,26 +73,28 @@ int dtype_size(int32_t dt) {
     }
 }
 
-}  // namespace
-}  // namespace crumpet
-
-extern "C" size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N) {
+size_t table_bytes(int64_t Hh, int64_t N, int ntables) {
     if (Hh <= 0 || N <= 0) return 0;
-    const int nt = crumpet::attn::select_tiles(N);
+    const int nt = attn::select_tiles(N);
     if (nt < 0) return 0;
     const int64_t np = 16 * nt;
-    return static_cast<size_t>(Hh * np * np * int64_t(sizeof(float)));
+    return static_cast<size_t>(ntables * Hh * np * np * int64_t(sizeof(float)));
 }
 
-extern "C" int crumpet_fused_swin_attention(
-    void* out, const int64_t out_strides[4], const void* q, const int64_t q_strides[4],
-    const void* k, const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
-    int32_t dtype, int64_t B, int64_t Hh, int64_t N, int64_t Dh, const void* bias,
-    int32_t bias_dtype, const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
-    int64_t mask_batch, const int64_t mask_strides[3], const uint8_t* boundary, float scale,
-    void* workspace, size_t workspace_bytes, void* stream) {
-    using namespace crumpet;
-    const char* what = "crumpet_fused_swin_attention";
+struct Region {
+    int64_t D, H, W, ws[3], ss[3];
+};
+
+// Shared path of both entry points.  mask/boundary describe tensor mode;
+// region (nullable) selects region mode.
+int run_attention(const char* what, void* out, const int64_t out_strides[4], const void* q,
+                  const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
+                  const void* v, const int64_t v_strides[4], int32_t dtype, int64_t B, int64_t Hh,
+                  int64_t N, int64_t Dh, const void* bias, int32_t bias_dtype,
+                  const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
+                  int64_t mask_batch, const int64_t mask_strides[3], const uint8_t* boundary,
+                  const Region* region, float scale, void* workspace, size_t workspace_bytes,
+                  void* stream) {
     const int esize = dtype_size(dtype);
     if (esize == 0) return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported dtype %d", what, dtype);
     if (B < 0 || Hh < 0 || N < 0 || Dh <= 0)
@@ -81,7 +106,7 @@ extern "C" int crumpet_fused_swin_attention(
     if (N > 512)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: N = %lld exceeds 512 tokens per window", what,
                     (long long)N);
-    if (B * Hh > 0x7fffffffLL)
+    if (B * Hh > 0x7fffffffLL || B > 0x3fffffffLL)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: too many (window, head) pairs", what);
     if (!out || !q || !k || !v || !bias || !out_strides || !q_strides || !k_strides ||
         !v_strides || !bias_strides)
@@ -105,7 +130,63 @@ extern "C" int crumpet_fused_swin_attention(
                         "%s: mask batch %lld must divide the window batch %lld", what,
                         (long long)mask_batch, (long long)B);
     }
-    const size_t need = crumpet_fused_swin_attention_workspace_size(Hh, N);
+
+    attn::Params p = {};
+    RegionCls rc = {1, 1, 1, 0, 0, 0};
+    int ntables = 1;
+    if (region != nullptr) {
+        const Region& rg = *region;
+        for (int a = 0; a < 3; ++a) {
+            if (rg.ws[a] <= 0 || rg.ss[a] < 0 || rg.ss[a] >= rg.ws[a])
+                return fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                            "%s: shift_size must satisfy 0 <= shift < window_size", what);
+        }
+        if (rg.D <= 0 || rg.H <= 0 || rg.W <= 0 || rg.D % rg.ws[0] || rg.H % rg.ws[1] ||
+            rg.W % rg.ws[2])
+            return fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                        "%s: D, H and W must be divisible by window_size", what);
+        if (rg.ws[0] * rg.ws[1] * rg.ws[2] != N)
+            return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: window volume must equal N", what);
+        const int64_t nWd = rg.D / rg.ws[0], nWh = rg.H / rg.ws[1], nWw = rg.W / rg.ws[2];
+        const int64_t nW = nWd * nWh * nWw;
+        if (B % nW != 0)
+            return fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                        "%s: window batch %lld must be a multiple of the %lld windows per volume",
+                        what, (long long)B, (long long)nW);
+        p.nWd = nWd;
+        p.nWh = nWh;
+        p.nWw = nWw;
+        p.nW = nW;
+        const int64_t batches = B / nW;
+        const int64_t nwin[3] = {nWd, nWh, nWw};
+        int nt = 0;
+        int64_t off = 0;
+        for (int code = 0; code < 8; ++code) {
+            int64_t ch[3];
+            bool ok = true;
+            for (int a = 0; a < 3; ++a) {
+                const bool last = (code >> (2 - a)) & 1;
+                const bool shifted = rg.ss[a] > 0;
+                if (last && !shifted) ok = false;
+                ch[a] = last ? 1 : (shifted ? nwin[a] - 1 : nwin[a]);
+            }
+            if (!ok) continue;
+            const int64_t count = ch[0] * ch[1] * ch[2] * batches;
+            if (count == 0) continue;
+            p.types.code[nt] = code;
+            for (int a = 0; a < 3; ++a) p.types.choices[nt][a] = static_cast<int32_t>(ch[a]);
+            p.types.offset[nt] = static_cast<int32_t>(off);
+            off += count;
+            ++nt;
+        }
+        p.types.ntypes = nt;
+        p.types.offset[nt] = static_cast<int32_t>(off);
+        rc = {int32_t(rg.ws[0]), int32_t(rg.ws[1]), int32_t(rg.ws[2]),
+              int32_t(rg.ss[0]), int32_t(rg.ss[1]), int32_t(rg.ss[2])};
+        ntables = 8;
+    }
+
+    const size_t need = table_bytes(Hh, N, ntables);
     if (workspace == nullptr || workspace_bytes < need ||
         reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT,
@@ -113,15 +194,17 @@ extern "C" int crumpet_fused_swin_attention(
 
     const int NT = attn::select_tiles(N);
     const int NP = 16 * NT;
-    attn::Params p;
-    p.q = q; p.k = k; p.v = v; p.out = out;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.out = out;
     for (int i = 0; i < 4; ++i) {
         p.qs[i] = q_strides[i];
         p.ks[i] = k_strides[i];
         p.vs[i] = v_strides[i];
         p.os[i] = out_strides[i];
     }
-    p.bias_ws = static_cast<const float*>(workspace);
+    p.table = static_cast<const float*>(workspace);
     p.mask = mask;
     for (int i = 0; i < 3; ++i) p.ms[i] = mask ? mask_strides[i] : 0;
     p.mask_batch = mask ? static_cast<int32_t>(mask_batch) : 1;
@@ -131,6 +214,17 @@ extern "C" int crumpet_fused_swin_attention(
     p.H = static_cast<int32_t>(Hh);
     p.N = static_cast<int32_t>(N);
     p.strips = static_cast<int32_t>((N + 15) / 16);
+    p.groups = (p.strips + attn::kWaves - 1) / attn::kWaves;
+    const int64_t units = Hh * p.groups;
+    int64_t wpw = (B * units + kTargetWorkgroups - 1) / kTargetWorkgroups;
+    if (wpw < 1) wpw = 1;
+    p.win_per_wg = static_cast<int32_t>(wpw);
+    p.ranges = static_cast<int32_t>((B + wpw - 1) / wpw);
+    const int64_t chunks = int64_t(p.ranges) * units;
+    if (chunks > 0x7fffffffLL)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: too many workgroups", what);
+    p.chunks = static_cast<uint32_t>(chunks);
+    p.launched = xcd_launch_count(p.chunks);
 
     // 4-element vector IO needs unit d stride, 4-element aligned row strides and bases.
     bool vec = true;
@@ -142,31 +236,31 @@ extern "C" int crumpet_fused_swin_attention(
             vec = false;
     }
     p.vec_io = vec ? 1 : 0;
-    p.chunks = static_cast<uint32_t>(B * Hh);
-    p.launched = xcd_launch_count(p.chunks);
 
     hipStream_t s = static_cast<hipStream_t>(stream);
     {
-        const int64_t total = Hh * NP * NP;
+        const int64_t total = int64_t(ntables) * Hh * NP * NP;
         int64_t blocks = (total + kPrepThreads - 1) / kPrepThreads;
-        if (blocks > 4096) blocks = 4096;
+        if (blocks > 8192) blocks = 8192;
         float* ws = static_cast<float*>(workspace);
+        const int32_t reg = region != nullptr ? 1 : 0;
         if (bias_dtype == CRUMPET_DTYPE_F16)
-            hipLaunchKernelGGL(bias_prep_kernel<_Float16>, dim3(blocks), dim3(kPrepThreads), 0, s, ws,
-                               static_cast<const _Float16*>(bias), bias_strides[0],
-                               bias_strides[1], bias_strides[2], p.H, p.N, NP);
+            hipLaunchKernelGGL(table_prep_kernel<_Float16>, dim3(blocks), dim3(kPrepThreads), 0, s,
+                               ws, static_cast<const _Float16*>(bias), bias_strides[0],
+                               bias_strides[1], bias_strides[2], p.H, p.N, NP, ntables, reg, rc);
         else if (bias_dtype == CRUMPET_DTYPE_BF16)
-            hipLaunchKernelGGL(bias_prep_kernel<__bf16>, dim3(blocks), dim3(kPrepThreads), 0, s, ws,
-                               static_cast<const __bf16*>(bias), bias_strides[0],
-                               bias_strides[1], bias_strides[2], p.H, p.N, NP);
+            hipLaunchKernelGGL(table_prep_kernel<__bf16>, dim3(blocks), dim3(kPrepThreads), 0, s,
+                               ws, static_cast<const __bf16*>(bias), bias_strides[0],
+                               bias_strides[1], bias_strides[2], p.H, p.N, NP, ntables, reg, rc);
         else
-            hipLaunchKernelGGL(bias_prep_kernel<float>, dim3(blocks), dim3(kPrepThreads), 0, s, ws,
-                               static_cast<const float*>(bias), bias_strides[0], bias_strides[1],
-                               bias_strides[2], p.H, p.N, NP);
+            hipLaunchKernelGGL(table_prep_kernel<float>, dim3(blocks), dim3(kPrepThreads), 0, s,
+                               ws, static_cast<const float*>(bias), bias_strides[0],
+                               bias_strides[1], bias_strides[2], p.H, p.N, NP, ntables, reg, rc);
         const int st2 = check_launch(what);
         if (st2 != CRUMPET_OK) return st2;
     }
-    const int kmask = mask == nullptr                     ? attn::kNoMask
+    const int kmask = region != nullptr                  ? attn::kMaskRegion
+                      : mask == nullptr                  ? attn::kNoMask
                       : mask_dtype == CRUMPET_DTYPE_F32  ? attn::kMaskF32
                       : mask_dtype == CRUMPET_DTYPE_BF16 ? attn::kMaskBF16
                                                          : attn::kMaskF16;
@@ -177,4 +271,43 @@ extern "C" int crumpet_fused_swin_attention(
     else
         attn::launch_f32(p, NT, kmask, s);
     return check_launch(what);
+}
+
+}  // namespace
+}  // namespace crumpet
+
+extern "C" size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N) {
+    return crumpet::table_bytes(Hh, N, 1);
+}
+
+extern "C" size_t crumpet_fused_swin_attention_shifted_workspace_size(int64_t Hh, int64_t N) {
+    return crumpet::table_bytes(Hh, N, 8);
+}
+
+extern "C" int crumpet_fused_swin_attention(
+    void* out, const int64_t out_strides[4], const void* q, const int64_t q_strides[4],
+    const void* k, const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+    int32_t dtype, int64_t B, int64_t Hh, int64_t N, int64_t Dh, const void* bias,
+    int32_t bias_dtype, const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
+    int64_t mask_batch, const int64_t mask_strides[3], const uint8_t* boundary, float scale,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    return crumpet::run_attention("crumpet_fused_swin_attention", out, out_strides, q, q_strides,
+                                  k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
+                                  bias_dtype, bias_strides, mask, mask_dtype, mask_batch,
+                                  mask_strides, boundary, nullptr, scale, workspace,
+                                  workspace_bytes, stream);
+}
+
+extern "C" int crumpet_fused_swin_attention_shifted(
+    void* out, const int64_t out_strides[4], const void* q, const int64_t q_strides[4],
+    const void* k, const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+    int32_t dtype, int64_t B, int64_t Hh, int64_t N, int64_t Dh, const void* bias,
+    int32_t bias_dtype, const int64_t bias_strides[3], int64_t D, int64_t H, int64_t W,
+    int64_t ws_d, int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w,
+    float scale, void* workspace, size_t workspace_bytes, void* stream) {
+    const crumpet::Region rg = {D, H, W, {ws_d, ws_h, ws_w}, {ss_d, ss_h, ss_w}};
+    return crumpet::run_attention("crumpet_fused_swin_attention_shifted", out, out_strides, q,
+                                  q_strides, k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
+                                  bias_dtype, bias_strides, nullptr, 0, 1, nullptr, nullptr, &rg,
+                                  scale, workspace, workspace_bytes, stream);
 }

@@ -1,18 +1,33 @@
 // Fused 3D Swin window attention kernel for gfx950 (MFMA 16x16 tiles, wave64).
 //
 // Per window b and head h:
-//   S   = (q * scale) k^T + bias[h] + (boundary[b] ? mask[b mod M] : 0)
+//   S   = (q * scale) k^T + bias[h] + mask_b
 //   out = softmax_rows(S) v
+// where mask_b is, depending on the mode,
+//   tensor : boundary[b] ? mask[b mod M] : 0          (a mask tensor)
+//   region : the shifted-window mask of window b      (from the geometry)
+//   none   : 0
 //
-// Work decomposition
-//   One workgroup (4 waves) per (window, head).  K and V of that pair are
-//   staged once in LDS (K row-major, V transposed), zero-padded to 16*NT
-//   keys.  Each wave then owns 16-query strips.  For a strip it computes the
-//   transposed score block S^T = K Q^T tile by tile, one MFMA per 16 keys x
-//   16 queries; the accumulator input is the bias tile (plus the mask tile on
-//   boundary windows), so those adds cost no VALU work.  The whole strip row
-//   (NT * 16 keys) stays in registers, so the softmax is an exact two-pass
-//   one (max, then exp2 and sum) with no online rescaling.
+// Work decomposition (bias-stationary, persistent)
+//   The relative-position bias is the same for every window, so it is kept in
+//   registers instead of being re-read per window: a workgroup of 4 waves
+//   owns one head h and a group of 4 consecutive 16-query strips, and walks a
+//   contiguous range of windows.  Each wave loads the fp32 bias tiles of its
+//   strip (NT tiles of 16 keys x 16 queries, 4 values per lane each) once and
+//   uses them as the accumulator input of every window's S^T = K Q^T MFMAs,
+//   so the bias add costs neither memory traffic nor VALU work.
+//
+//   Q (the group's 64 rows, pre-scaled and rounded), K (row-major) and V
+//   (transposed) of a window live in LDS, double-buffered: while the waves
+//   compute window i, each thread holds its share of window i+1 in registers
+//   and writes it to the other buffer afterwards; one barrier per window.
+//
+//   In region mode the windows are visited grouped by type (which axes the
+//   window is last on; at most 8 types).  The shifted-window mask of a window
+//   depends only on its type, so the host prepares bias+mask tables per type
+//   and a type change is just a register reload - the mask costs nothing per
+//   window.  Logical index -> window uses per-type offsets and mixed-radix
+//   decoding (Params::types).
 //
 // Layout trick
 //   In the 16x16 MFMA output a lane holds 4 consecutive rows of one column.
@@ -20,27 +35,21 @@
 //   l%16, which is exactly the B-operand layout of the second product
 //   O^T = V^T P^T.  P therefore never leaves registers: it is rounded to the
 //   input type in place and fed straight into v_mfma_f32_16x16x32_{f16,bf16}
-//   (two key tiles per instruction).  O^T lands as 4 consecutive head-dim
-//   values of one query per lane, which is one 8-byte store.
-//
-// Control flow
-//   The tile count NT is a template parameter (one of kTileCounts) and the
-//   masked / unmasked strip bodies are separate instantiations chosen once
-//   per workgroup, so the unrolled tile loop has no per-tile branches.
-//   Padded query rows load the last real row (their output is never
-//   stored); mask loads go through a buffer descriptor bounded by the
-//   window, so padded keys need no test either (their bias is -inf).
+//   (two key tiles per instruction); the row sums ride on the same pipe as
+//   ones^T P^T.  O^T lands as 4 consecutive head-dim values of one query per
+//   lane, which is one 8-byte store.
 //
 // Padding
-//   The bias is first copied into a padded fp32 workspace [H][NP][NP]
-//   (NP = 16*NT) whose padded key columns hold -inf (probability exactly 0)
-//   and whose padded query rows hold 0.
+//   Workspace tables are [T][H][NP][NP] fp32 (NP = 16*NT); padded key
+//   columns hold -inf (probability exactly 0), padded query rows 0.  K, V and
+//   Q rows past N are zero in LDS.
 //
 // Numerics follow torch-ext/crumpet/fused_attention.py:82-146: q is scaled
 // in fp32 and rounded back to the input type, products accumulate in fp32,
-// bias then mask are added in fp32, the row sum is taken over fp32
-// probabilities, P is rounded (RNE) to the input type before the second
-// product, and the output is acc / rowsum rounded to the output type.
+// bias and mask are added in fp32, P is rounded (RNE) to the input type
+// before the second product, and the output is acc / rowsum rounded to the
+// output type.  The row sum is taken over the rounded P (the same values the
+// numerator uses).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -53,23 +62,20 @@
 namespace crumpet {
 namespace attn {
 
-// Per-dtype entry points (one translation unit each, compiled in parallel).
-struct Params;
-void launch_f16(const Params& p, int NT, int kmask, hipStream_t s);
-void launch_bf16(const Params& p, int NT, int kmask, hipStream_t s);
-void launch_f32(const Params& p, int NT, int kmask, hipStream_t s);
-
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr int kWaves = 4;  // waves (strips) per workgroup
+constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
+// Mask modes (template parameter kMask).
+enum MaskKind { kNoMask = 0, kMaskF16 = 1, kMaskF32 = 2, kMaskBF16 = 3, kMaskRegion = 4 };
+
+// Window-type table of region mode: logical window index -> window.
+struct TypeTable {
+    int32_t ntypes;
+    int32_t offset[9];     // first logical index of each type (offset[ntypes] = B)
+    int32_t code[8];       // 3-bit type code: bit2 = last along D, bit1 = H, bit0 = W
+    int32_t choices[8][3]; // window choices per axis for the type
+};
 
 struct Params {
     const void* q;
@@ -77,17 +83,28 @@ struct Params {
     const void* v;
     void* out;
     int64_t qs[4], ks[4], vs[4], os[4];  // element strides (b, h, n, d)
-    const float* bias_ws;                // [H][NP][NP] fp32, NP = 16 * NT
-    const void* mask;                    // [M][N][N] or null, unit key stride
+    const float* table;                  // [T][H][NP][NP] fp32 bias (+ mask per type)
+    const void* mask;                    // tensor mode: [M][N][N], unit key stride
     int64_t ms[3];
     int32_t mask_batch;
-    const uint8_t* boundary;
+    const uint8_t* boundary;  // tensor mode: [B] flags or null
     float scale;
     int32_t B, H, N;
-    int32_t strips;  // ceil(N / 16)
-    int32_t vec_io;  // q/k/v/out rows are 4-element aligned with unit d stride
+    int32_t strips;          // ceil(N / 16)
+    int32_t groups;          // ceil(strips / kWaves)
+    int32_t win_per_wg;      // windows walked by one workgroup
+    int32_t ranges;          // ceil(B / win_per_wg)
+    int32_t vec_io;          // q/k/v/out rows are 4-element aligned with unit d stride
     uint32_t chunks, launched;
+    // region mode geometry
+    int32_t nWd, nWh, nWw, nW;  // windows per volume along D, H, W and in total
+    TypeTable types;
 };
+
+// Per-dtype entry points (one translation unit each, compiled in parallel).
+void launch_f16(const Params& p, int NT, int kmask, hipStream_t s);
+void launch_bf16(const Params& p, int NT, int kmask, hipStream_t s);
+void launch_f32(const Params& p, int NT, int kmask, hipStream_t s);
 
 // Tile counts the kernel is compiled for; a call runs with the smallest one
 // that covers ceil(N / 16).
@@ -99,6 +116,13 @@ inline int select_tiles(int64_t N) {
         if (c >= need) return c;
     return -1;
 }
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 // Kernels and device helpers have internal linkage: every translation unit
 // that instantiates them gets its own copy, and none is exported.
@@ -137,54 +161,154 @@ struct Frag<float> {
     typedef f32x4 x4;
 };
 
-// 4 consecutive head-dim elements (d0..d0+3) of one row.
-template <typename T>
-__device__ __forceinline__ typename Frag<T>::x4 load_row4(const T* row, int64_t sd, int d0, bool vec) {
+// 4 consecutive head-dim elements (d0..d0+3) of one row: one vector load
+// when rows have unit d stride and 4-element alignment (kVec), else 4 loads.
+template <typename T, bool kVec>
+__device__ __forceinline__ typename Frag<T>::x4 load_row4(const T* row, int64_t sd, int d0) {
     typedef typename Frag<T>::x4 X4;
-    if (vec) return *reinterpret_cast<const X4*>(row + d0);
-    X4 r;
+    if constexpr (kVec) {
+        return *reinterpret_cast<const X4*>(row + d0);
+    } else {
+        X4 r;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r[e] = row[(d0 + e) * sd];
+        for (int e = 0; e < 4; ++e) r[e] = row[(d0 + e) * sd];
+        return r;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::x4 zero4() {
+    typename Frag<T>::x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) r[e] = T(0.0f);
     return r;
 }
 
-// Waves per SIMD the register allocation targets; the strip's score row
-// (NT * 4 fp32 per lane) dominates the budget.
-template <typename T, int NT, int kMask>
+// Waves per SIMD the register allocation targets: the strip's bias tiles and
+// score row (2 * NT * 4 fp32 per lane) dominate the budget.
+template <int NT>
 constexpr int waves_per_eu() {
-    return NT <= 8 ? 4 : (NT <= 22 ? 3 : 2);
+    return NT <= 4 ? 4 : (NT <= 8 ? 3 : 2);
 }
 
-// Mask storage types (template parameter kMask).
-enum MaskKind { kNoMask = 0, kMaskF16 = 1, kMaskF32 = 2, kMaskBF16 = 3 };
+// Logical window index -> window index b (region mode visits windows by type).
+template <int kMask>
+__device__ __forceinline__ int window_of(const Params& p, int i, int& type_code) {
+    if constexpr (kMask != kMaskRegion) {
+        type_code = 0;
+        return i;
+    } else {
+        int t = 0;
+        while (t + 1 < p.types.ntypes && i >= p.types.offset[t + 1]) ++t;
+        const int code = p.types.code[t];
+        const int cd = p.types.choices[t][0], ch = p.types.choices[t][1], cw = p.types.choices[t][2];
+        int j = i - p.types.offset[t];
+        const int per = cd * ch * cw;
+        const int batch = j / per;
+        j -= batch * per;
+        const int jw = j % cw;
+        j /= cw;
+        const int jh = j % ch;
+        const int jd = j / ch;
+        const int wd = (code & 4) ? p.nWd - 1 : jd;
+        const int wh = (code & 2) ? p.nWh - 1 : jh;
+        const int ww = (code & 1) ? p.nWw - 1 : jw;
+        type_code = code;
+        return batch * p.nW + (wd * p.nWh + wh) * p.nWw + ww;
+    }
+}
 
-// One 16-query strip s of window b, head h.  q_lds holds Q already scaled
-// and rounded, K row-major, V transposed; padded rows/keys are zero.
-template <typename T, int NT, int kMask, bool kUseMask>
-__device__ __forceinline__ void attend_strip(const Params& p, const T* __restrict__ q_lds,
-                                             const T* __restrict__ k_lds,
-                                             const T* __restrict__ vt_lds, int vt_stride, T* ob,
-                                             int b, int h, int s, int col, int g, bool vec) {
+// Staging of one window's Q (this group's rows), K and V into LDS.  Each
+// thread owns chunks c = tid + k * kThreads of 4 elements; kQChunks Q chunks
+// come first, then NP*4 K chunks, then NP*4 V chunks.
+template <typename T, int NT, bool kVec>
+struct Stage {
+    static constexpr int NP = NT * 16;
+    static constexpr int kQRows = 16 * kWaves;
+    static constexpr int kQChunks = kQRows * 4;
+    static constexpr int kChunks = kQChunks + 2 * NP * 4;
+    static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kVtStride = NP + 4;  // keeps 8/16-byte rows, breaks bank aliasing
     typedef typename Frag<T>::x4 X4;
-    constexpr int NP = NT * 16;
+
+    X4 r[kPerThread];
+
+    __device__ __forceinline__ void load(const Params& p, int b, int h, int q0) {
+        const T* qb = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
+        const T* kb = static_cast<const T*>(p.k) + b * p.ks[0] + h * p.ks[1];
+        const T* vb = static_cast<const T*>(p.v) + b * p.vs[0] + h * p.vs[1];
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k) {
+            const int c = threadIdx.x + k * kThreads;
+            r[k] = zero4<T>();
+            if (c < kQChunks) {
+                const int n = q0 + (c >> 2);
+                if (n < p.N) {
+                    r[k] = load_row4<T, kVec>(qb + n * p.qs[2], p.qs[3], (c & 3) * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) r[k][e] = T(static_cast<float>(r[k][e]) * p.scale);
+                }
+            } else if (c < kChunks) {
+                const int cc = c - kQChunks;
+                const bool isv = cc >= NP * 4;
+                const int c2 = isv ? cc - NP * 4 : cc;
+                const int n = c2 >> 2;
+                if (n < p.N)
+                    r[k] = isv ? load_row4<T, kVec>(vb + n * p.vs[2], p.vs[3], (c2 & 3) * 4)
+                               : load_row4<T, kVec>(kb + n * p.ks[2], p.ks[3], (c2 & 3) * 4);
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(T* q_lds, T* k_lds, T* vt_lds) const {
+#pragma unroll
+        for (int k = 0; k < kPerThread; ++k) {
+            const int c = threadIdx.x + k * kThreads;
+            if (c < kQChunks) {
+                *reinterpret_cast<X4*>(&q_lds[c * 4]) = r[k];
+            } else if (c < kChunks) {
+                const int cc = c - kQChunks;
+                if (cc < NP * 4) {
+                    *reinterpret_cast<X4*>(&k_lds[cc * 4]) = r[k];
+                } else {
+                    const int c2 = cc - NP * 4;
+                    const int n = c2 >> 2, d0 = (c2 & 3) * 4;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n] = r[k][e];
+                }
+            }
+        }
+    }
+};
+
+// Bias (+ region mask) tiles of one strip: rows qi of the table, 4 keys per lane per tile.
+template <int NT>
+__device__ __forceinline__ void load_tiles(f32x4 (&bs)[NT], const float* row) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) bs[t] = *reinterpret_cast<const f32x4*>(row + 16 * t);
+}
+
+// One strip (16 queries, NT*16 keys) of one window.
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec>
+__device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
+                                       const T* __restrict__ k_lds, const T* __restrict__ vt_lds,
+                                       int b, int h, int wave, int qi, int col, int g) {
+    typedef typename Frag<T>::x4 X4;
+    constexpr int kVtStride = Stage<T, NT, kVec>::kVtStride;
+    constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
     constexpr int kPrefetch = NT < 6 ? NT : 6;
     const int N = p.N;
-    const int qi = s * 16 + col;
 
-    // B operand of S^T = K Q^T: Q[qi][4g..4g+3]
-    const X4 qf = *reinterpret_cast<const X4*>(&q_lds[qi * 16 + 4 * g]);
+    // B operand of S^T = K Q^T: Q[qi][4g..4g+3] (pre-scaled in LDS)
+    const X4 qf = *reinterpret_cast<const X4*>(&q_lds[(wave * 16 + col) * 16 + 4 * g]);
 
-    const float* brow = p.bias_ws + (int64_t(h) * NP + qi) * NP + 4 * g;
-
-    // Mask of this window read through a buffer descriptor spanning exactly
-    // the window's [N, N] extent: offsets past it return 0 in hardware, so the
-    // loads need no per-key test.  Padded keys of a row read a finite
-    // neighbour value, harmless under their -inf bias; padded query rows read
-    // row N-1 and are never stored.  Per-tile offsets are instruction
-    // immediates.
-    constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
+    // Tensor mask through a buffer descriptor spanning exactly the window's
+    // [N, N] extent: offsets past it return 0, so no per-key test is needed;
+    // padded keys read a finite neighbour (their bias is -inf) and padded
+    // query rows read row N-1 (never stored).  Offsets are immediates.
     __amdgpu_buffer_rsrc_t mrsrc;
     int mvoff = 0;
+    uint32_t mq[kUseMask ? 4 * kPrefetch : 1];
     if constexpr (kUseMask) {
         const int qr = qi < N ? qi : N - 1;
         const char* mbase = static_cast<const char*>(p.mask) +
@@ -193,12 +317,7 @@ __device__ __forceinline__ void attend_strip(const Params& p, const T* __restric
         mrsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mbase), 0, extent, 0x00020000);
         mvoff = static_cast<int>((qr * p.ms[1] + 4 * g) * kMaskBytes);
     }
-
-    // accumulator input of tile t, fetched kPrefetch tiles ahead
-    f32x4 bq[kPrefetch];
-    uint32_t mq[kUseMask ? 4 * kPrefetch : 1];
     auto fetch = [&](int t, int slot) {
-        bq[slot] = *reinterpret_cast<const f32x4*>(brow + 16 * t);
         if constexpr (kUseMask) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -210,125 +329,162 @@ __device__ __forceinline__ void attend_strip(const Params& p, const T* __restric
             }
         }
     };
+    if constexpr (kUseMask) {
 #pragma unroll
-    for (int t = 0; t < kPrefetch; ++t) fetch(t, t);
-
-    f32x4 S[NT];
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        const int slot = t % kPrefetch;
-        f32x4 c = bq[slot];
-        if constexpr (kUseMask) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t bits = mq[4 * slot + r];
-                if constexpr (kMask == kMaskF16)
-                    c[r] += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-                else if constexpr (kMask == kMaskBF16)
-                    c[r] += __uint_as_float(bits << 16);
-                else
-                    c[r] += __uint_as_float(bits);
-            }
-        }
-        if (t + kPrefetch < NT) fetch(t + kPrefetch, slot);
-        if constexpr (sizeof(T) == 2) {
-            const X4 kf = *reinterpret_cast<const X4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
-            S[t] = Frag<T>::mma16(kf, qf, c);
-        } else {
-            const f32x4 kf = *reinterpret_cast<const f32x4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
-            f32x4 acc = c;
-#pragma unroll
-            for (int kk = 0; kk < 4; ++kk)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kk], qf[kk], acc, 0, 0, 0);
-            S[t] = acc;
-        }
-        // keep the ring: no load of a later tile may be hoisted above this point
-        __builtin_amdgcn_sched_barrier(0);
+        for (int t = 0; t < kPrefetch; ++t) fetch(t, t);
     }
 
-    // exact row max over all keys: two 3-input maxes per tile on two
-    // independent chains, then across the 4 lane groups
-    float m0 = -INFINITY, m1 = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        if (t & 1) {
-            m1 = fmaxf(fmaxf(m1, S[t][0]), S[t][1]);
-            m1 = fmaxf(fmaxf(m1, S[t][2]), S[t][3]);
-        } else {
-            m0 = fmaxf(fmaxf(m0, S[t][0]), S[t][1]);
-            m0 = fmaxf(fmaxf(m0, S[t][2]), S[t][3]);
-        }
-    }
-    float m = fmaxf(m0, m1);
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
-    const float mb = m * kLog2e;
-
-#pragma unroll
-    for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) S[t][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[t][r], kLog2e, -mb));
-
-    // O^T = V^T P^T; the row sums ride on the matrix pipe as ones^T P^T
+    // Keys are processed in chunks of at most kChunk tiles with an online
+    // softmax between chunks (running max, rescaled O and row sums), which
+    // keeps only one chunk of scores in registers next to the bias tiles.
+    constexpr int kNumChunks = (NT + 11) / 12;
+    constexpr int kChunk = (NT + kNumChunks - 1) / kNumChunks;
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    float l;
-    const T* vrow = &vt_lds[col * vt_stride + 4 * g];
-    if constexpr (sizeof(T) == 2) {
-        typedef typename Frag<T>::x8 X8;
-        f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
-        X8 ones8;
-        X4 ones4;
+    f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float lsum = 0.0f;  // fp32 path row sum (VALU)
+    float m_run = -INFINITY;
+    const T* vrow = &vt_lds[col * kVtStride + 4 * g];
+
 #pragma unroll
-        for (int r = 0; r < 8; ++r) ones8[r] = T(1.0f);
+    for (int c0 = 0; c0 < NT; c0 += kChunk) {
+        // chunks must not interleave: that would keep two chunks of scores live
+        __builtin_amdgcn_sched_barrier(0);
+        const int cn = (NT - c0 < kChunk) ? NT - c0 : kChunk;
+        f32x4 S[kChunk];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ones4[r] = T(1.0f);
+        for (int u = 0; u < kChunk; ++u) {
+            if (u >= cn) break;
+            const int t = c0 + u;
+            f32x4 c = bs[t];
+            if constexpr (kUseMask) {
+                const int slot = t % kPrefetch;
 #pragma unroll
-        for (int t = 0; t + 1 < NT; t += 2) {
-            X8 pb, va;
-            const X4 v0 = *reinterpret_cast<const X4*>(vrow + 16 * t);
-            const X4 v1 = *reinterpret_cast<const X4*>(vrow + 16 * t + 16);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                pb[r] = T(S[t][r]);
-                pb[r + 4] = T(S[t + 1][r]);
-                va[r] = v0[r];
-                va[r + 4] = v1[r];
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t bits = mq[4 * slot + r];
+                    if constexpr (kMask == kMaskF16)
+                        c[r] += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+                    else if constexpr (kMask == kMaskBF16)
+                        c[r] += __uint_as_float(bits << 16);
+                    else
+                        c[r] += __uint_as_float(bits);
+                }
+                if (t + kPrefetch < NT) fetch(t + kPrefetch, slot);
             }
-            o = Frag<T>::mma32(va, pb, o);
-            lacc = Frag<T>::mma32(ones8, pb, lacc);
-        }
-        if constexpr (NT % 2 == 1) {
-            X4 pb;
+            if constexpr (sizeof(T) == 2) {
+                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
+                S[u] = Frag<T>::mma16(kf, qf, c);
+            } else {
+                const f32x4 kf = *reinterpret_cast<const f32x4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
+                f32x4 acc = c;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pb[r] = T(S[NT - 1][r]);
-            const X4 v0 = *reinterpret_cast<const X4*>(vrow + 16 * (NT - 1));
-            o = Frag<T>::mma16(v0, pb, o);
-            lacc = Frag<T>::mma16(ones4, pb, lacc);
+                for (int kk = 0; kk < 4; ++kk)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kk], qf[kk], acc, 0, 0, 0);
+                S[u] = acc;
+            }
+            if constexpr (kUseMask) __builtin_amdgcn_sched_barrier(0);  // keep the mask ring
         }
+
+        // chunk row max: two 3-input maxes per tile on two independent chains,
+        // then across the 4 lane groups
+        float m0 = m_run, m1 = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            if (u >= cn) break;
+            if (u & 1) {
+                m1 = fmaxf(fmaxf(m1, S[u][0]), S[u][1]);
+                m1 = fmaxf(fmaxf(m1, S[u][2]), S[u][3]);
+            } else {
+                m0 = fmaxf(fmaxf(m0, S[u][0]), S[u][1]);
+                m0 = fmaxf(fmaxf(m0, S[u][2]), S[u][3]);
+            }
+        }
+        float m = fmaxf(m0, m1);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const float mb = m * kLog2e;
+        if (c0 > 0) {  // rescale what the earlier chunks accumulated
+            const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, kLog2e, -mb));
+            o *= alpha;
+            lacc *= alpha;
+            lsum *= alpha;
+        }
+        m_run = m;
+
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) {
+            if (u >= cn) break;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) S[u][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[u][r], kLog2e, -mb));
+        }
+
+        // O^T += V^T P^T; the row sums ride on the matrix pipe as ones^T P^T
+        if constexpr (sizeof(T) == 2) {
+            typedef typename Frag<T>::x8 X8;
+            X8 ones8;
+#pragma unroll
+            for (int r = 0; r < 8; ++r) ones8[r] = T(1.0f);
+#pragma unroll
+            for (int u = 0; u + 1 < kChunk; u += 2) {
+                if (u + 1 >= cn) break;
+                const int t = c0 + u;
+                X8 pb, va;
+                const X4 v0 = *reinterpret_cast<const X4*>(vrow + 16 * t);
+                const X4 v1 = *reinterpret_cast<const X4*>(vrow + 16 * t + 16);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pb[r] = T(S[u][r]);
+                    pb[r + 4] = T(S[u + 1][r]);
+                    va[r] = v0[r];
+                    va[r + 4] = v1[r];
+                }
+                o = Frag<T>::mma32(va, pb, o);
+                lacc = Frag<T>::mma32(ones8, pb, lacc);
+            }
+            if (cn & 1) {
+                // odd tile: the same 16x16x32 instruction with a zero upper
+                // half, so each accumulator chain uses a single MFMA opcode
+                const int u = cn - 1;
+                X8 pb, va;
+                const X4 v0 = *reinterpret_cast<const X4*>(vrow + 16 * (c0 + u));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    pb[r] = T(S[u][r]);
+                    pb[r + 4] = T(0.0f);
+                    va[r] = v0[r];
+                    va[r + 4] = T(0.0f);
+                }
+                o = Frag<T>::mma32(va, pb, o);
+                lacc = Frag<T>::mma32(ones8, pb, lacc);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < kChunk; ++u) {
+                if (u >= cn) break;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(vrow + 16 * (c0 + u));
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    o = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[r], S[u][r], o, 0, 0, 0);
+                    lsum += S[u][r];
+                }
+            }
+        }
+    }
+    float l;
+    if constexpr (sizeof(T) == 2) {
         l = lacc[0];  // every row of ones^T P^T holds the sum for query col
     } else {
-        float ls = 0.0f;
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            const f32x4 v0 = *reinterpret_cast<const f32x4*>(vrow + 16 * t);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                o = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[r], S[t][r], o, 0, 0, 0);
-                ls += S[t][r];
-            }
-        }
-        ls += __shfl_xor(ls, 16);
-        l = ls + __shfl_xor(ls, 32);
+        lsum += __shfl_xor(lsum, 16);
+        l = lsum + __shfl_xor(lsum, 32);
     }
 
     // lane holds O[qi][4g + r], r = 0..3
     if (qi < N) {
-        T* orow = ob + qi * p.os[2];
+        T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
         const float inv = 1.0f / l;
         X4 res;
 #pragma unroll
         for (int r = 0; r < 4; ++r) res[r] = T(o[r] * inv);
-        if (vec) {
+        if constexpr (kVec) {
             *reinterpret_cast<X4*>(orow + 4 * g) = res;
         } else {
 #pragma unroll
@@ -337,82 +493,99 @@ __device__ __forceinline__ void attend_strip(const Params& p, const T* __restric
     }
 }
 
-template <typename T, int NT, int kMask>
+template <typename T, int NT, int kMask, bool kVec>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask>(), waves_per_eu<T, NT, kMask>())))
+__attribute__((amdgpu_waves_per_eu(waves_per_eu<NT>(), waves_per_eu<NT>())))
 swin_attention_d16_kernel(const Params p) {
-    typedef typename Frag<T>::x4 X4;
-    constexpr int NP = NT * 16;
-    constexpr int kVtStride = NP + 4;  // keeps 8/16-byte row alignment, breaks bank aliasing
-    __shared__ __attribute__((aligned(16))) T q_lds[NP * 16];
-    __shared__ __attribute__((aligned(16))) T k_lds[NP * 16];
-    __shared__ __attribute__((aligned(16))) T vt_lds[16 * kVtStride];
+    typedef Stage<T, NT, kVec> St;
+    constexpr int NP = St::NP;
+    __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * 16];
+    __shared__ __attribute__((aligned(16))) T k_lds[2][NP * 16];
+    __shared__ __attribute__((aligned(16))) T vt_lds[2][16 * St::kVtStride];
 
     uint32_t chunk;
     if (!xcd_chunk(blockIdx.x, p.launched, p.chunks, chunk)) return;
-    const int b = static_cast<int>(chunk / p.H);
-    const int h = static_cast<int>(chunk % p.H);
-    const int N = p.N;
-    const bool vec = p.vec_io != 0;
-
-    // ---- stage Q (scaled in fp32, rounded back), K (row-major) and V
-    //      (transposed) of this (b, h) in LDS; rows past N are zero ----
-    const T* qb = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
-    const T* kb = static_cast<const T*>(p.k) + b * p.ks[0] + h * p.ks[1];
-    const T* vb = static_cast<const T*>(p.v) + b * p.vs[0] + h * p.vs[1];
-    for (int c = threadIdx.x; c < NP * 4; c += kThreads) {
-        const int n = c >> 2;
-        const int d0 = (c & 3) * 4;
-        X4 qv, kv, vv;
-        if (n < N) {
-            qv = load_row4<T>(qb + n * p.qs[2], p.qs[3], d0, vec);
-            kv = load_row4<T>(kb + n * p.ks[2], p.ks[3], d0, vec);
-            vv = load_row4<T>(vb + n * p.vs[2], p.vs[3], d0, vec);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) qv[e] = T(static_cast<float>(qv[e]) * p.scale);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) qv[e] = kv[e] = vv[e] = T(0.0f);
-        }
-        *reinterpret_cast<X4*>(&q_lds[n * 16 + d0]) = qv;
-        *reinterpret_cast<X4*>(&k_lds[n * 16 + d0]) = kv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n] = vv[e];
-    }
-    __syncthreads();
+    // chunk = (range * H + h) * groups + group: the groups of one (range, head)
+    // are consecutive, hence on one XCD, and share its L2 for K/V.
+    const int grp = static_cast<int>(chunk % p.groups);
+    const int rh = static_cast<int>(chunk / p.groups);
+    const int h = rh % p.H;
+    const int range = rh / p.H;
+    const int i0 = range * p.win_per_wg;
+    const int i1 = min(p.B, i0 + p.win_per_wg);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int col = lane & 15;
     const int g = lane >> 4;
-    T* ob = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1];
-    const bool use_mask = kMask != kNoMask && (p.boundary == nullptr || p.boundary[b] != 0);
+    const int strip = grp * kWaves + wave;
+    const int qi = strip * 16 + col;
+    const bool active = strip < p.strips;
+    const int q0 = grp * kWaves * 16;  // first query row of this group
 
-    if constexpr (kMask != kNoMask) {
-        if (use_mask) {
-            for (int s = wave; s < p.strips; s += kWaves)
-                attend_strip<T, NT, kMask, true>(p, q_lds, k_lds, vt_lds, kVtStride, ob, b, h, s, col, g, vec);
-            return;
+    // this wave's table row: [type][h][qi][4g ...]
+    const size_t type_stride = size_t(p.H) * NP * NP;
+    const float* trow = p.table + (size_t(h) * NP + (active ? qi : 0)) * NP + 4 * g;
+
+    St st;
+    int code_cur = -1;
+    int code_next;
+    int b_next = window_of<kMask>(p, i0, code_next);
+    st.load(p, b_next, h, q0);
+    st.store(q_lds[0], k_lds[0], vt_lds[0]);
+    __syncthreads();
+
+    f32x4 bs[NT];
+    for (int i = i0; i < i1; ++i) {
+        const int buf = (i - i0) & 1;
+        const int b = b_next;
+        const int code = code_next;
+        if (i + 1 < i1) {
+            b_next = window_of<kMask>(p, i + 1, code_next);
+            st.load(p, b_next, h, q0);
         }
+        if (active) {
+            if (code != code_cur) {  // workgroup-uniform: new bias (+ mask) tiles
+                load_tiles<NT>(bs, trow + (kMask == kMaskRegion ? code * type_stride : 0));
+                code_cur = code;
+            }
+            bool use_mask = false;
+            if constexpr (kMask != kNoMask && kMask != kMaskRegion)
+                use_mask = p.boundary == nullptr || p.boundary[b] != 0;
+            if (use_mask)
+                attend<T, NT, kMask, (kMask != kNoMask && kMask != kMaskRegion), kVec>(
+                    p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h, wave, qi, col, g);
+            else
+                attend<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b,
+                                                  h, wave, qi, col, g);
+        }
+        if (i + 1 < i1) st.store(q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+        __syncthreads();
     }
-    for (int s = wave; s < p.strips; s += kWaves)
-        attend_strip<T, NT, kMask, false>(p, q_lds, k_lds, vt_lds, kVtStride, ob, b, h, s, col, g, vec);
 }
 
 // Launch for element type T; NT from kTileCounts, kmask a MaskKind.
 template <typename T>
 void launch(const Params& p, int NT, int kmask, hipStream_t s) {
     const dim3 grid(p.launched), block(kThreads);
-#define CRUMPET_ATTN_MASK(NTV, MK) \
-    hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK>), grid, block, 0, s, p)
-#define CRUMPET_ATTN_NT(NTV)                                        \
-    case NTV:                                                       \
-        switch (kmask) {                                            \
-            case kNoMask: CRUMPET_ATTN_MASK(NTV, kNoMask); break;   \
-            case kMaskF16: CRUMPET_ATTN_MASK(NTV, kMaskF16); break; \
-            case kMaskF32: CRUMPET_ATTN_MASK(NTV, kMaskF32); break; \
-            default: CRUMPET_ATTN_MASK(NTV, kMaskBF16); break;      \
-        }                                                           \
+#define CRUMPET_ATTN_MASK(NTV, MK)                                                              \
+    do {                                                                                        \
+        if (p.vec_io)                                                                           \
+            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true>), grid, block, 0, s,  \
+                               p);                                                              \
+        else                                                                                    \
+            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, false>), grid, block, 0, s, \
+                               p);                                                              \
+    } while (0)
+#define CRUMPET_ATTN_NT(NTV)                                            \
+    case NTV:                                                           \
+        switch (kmask) {                                                \
+            case kNoMask: CRUMPET_ATTN_MASK(NTV, kNoMask); break;       \
+            case kMaskF16: CRUMPET_ATTN_MASK(NTV, kMaskF16); break;     \
+            case kMaskF32: CRUMPET_ATTN_MASK(NTV, kMaskF32); break;     \
+            case kMaskBF16: CRUMPET_ATTN_MASK(NTV, kMaskBF16); break;   \
+            default: CRUMPET_ATTN_MASK(NTV, kMaskRegion); break;        \
+        }                                                               \
         break;
     switch (NT) {
         CRUMPET_ATTN_NT(1)
@@ -429,6 +602,5 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
 }
 
 }  // namespace
-
 }  // namespace attn
 }  // namespace crumpet

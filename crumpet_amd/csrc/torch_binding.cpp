@@ -2,7 +2,9 @@
 //
 // Same five op schemas and tags as the reference
 // (torch-ext/torch_binding.cpp:10-31), plus `fused_swin_attention`, which
-// the reference launched from Python through Triton.  Every impl checks
+// the reference launched from Python through Triton, and
+// `fused_swin_attention_shifted` (attention with the shifted-window mask
+// derived from the volume geometry instead of a mask tensor).  Every impl checks
 // shapes, dtypes and devices (so no launch can index outside its tensors),
 // takes the current HIP stream of the tensor's device (ROCm torch tags HIP
 // devices as "cuda", hence the masquerading guard/stream helpers) and forwards to the
@@ -192,6 +194,47 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
         ws.data_ptr(), ws_bytes, stream_of(q)));
 }
 
+void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
+                                  const at::Tensor& v, const at::Tensor& bias, int64_t D,
+                                  int64_t H, int64_t W, int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                  int64_t ss_d, int64_t ss_h, int64_t ss_w, double scale) {
+    const char* what = "fused_swin_attention_shifted";
+    TORCH_CHECK(q.dim() == 4, what, ": q must have shape [B, H, N, D]");
+    TORCH_CHECK(k.sizes() == q.sizes() && v.sizes() == q.sizes() && out.sizes() == q.sizes(), what,
+                ": q, k, v and out must have the same shape");
+    TORCH_CHECK(k.scalar_type() == q.scalar_type() && v.scalar_type() == q.scalar_type() &&
+                    out.scalar_type() == q.scalar_type(),
+                what, ": q, k, v and out must have the same dtype");
+    const int32_t dt = dtype_code(q.scalar_type());
+    TORCH_CHECK(dt >= 0, what, ": dtype must be float32, float16 or bfloat16");
+    const at::Device dev = q.device();
+    TORCH_CHECK(q.is_cuda() && k.device() == dev && v.device() == dev && out.device() == dev &&
+                    bias.device() == dev,
+                what, ": all tensors must be on the same HIP device");
+    const int64_t B = q.size(0), Hh = q.size(1), N = q.size(2), Dh = q.size(3);
+    TORCH_CHECK(bias.dim() == 3 && bias.size(0) == Hh && bias.size(1) == N && bias.size(2) == N,
+                what, ": relative_position_bias must have shape [H, N, N]");
+    const int32_t bdt = dtype_code(bias.scalar_type());
+    TORCH_CHECK(bdt >= 0, what, ": bias dtype must be float32, float16 or bfloat16");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
+    if (out.numel() == 0) return;
+    const size_t ws_bytes = crumpet_fused_swin_attention_shifted_workspace_size(Hh, N);
+    at::Tensor ws = at::empty({static_cast<int64_t>((ws_bytes + 15) / 16) * 4},
+                              q.options().dtype(at::kFloat));
+    int64_t qs[4], ks[4], vs[4], os[4], bs[3];
+    for (int i = 0; i < 4; ++i) {
+        qs[i] = q.stride(i);
+        ks[i] = k.stride(i);
+        vs[i] = v.stride(i);
+        os[i] = out.stride(i);
+    }
+    for (int i = 0; i < 3; ++i) bs[i] = bias.stride(i);
+    check_status(crumpet_fused_swin_attention_shifted(
+        out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
+        bias.data_ptr(), bdt, bs, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w,
+        static_cast<float>(scale), ws.data_ptr(), ws_bytes, stream_of(q)));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(crumpet_ops, ops) {
@@ -219,6 +262,11 @@ TORCH_LIBRARY(crumpet_ops, ops) {
         "fused_swin_attention(Tensor! out, Tensor q, Tensor k, Tensor v, Tensor bias, "
         "Tensor? mask, Tensor? boundary, float scale) -> ()",
         kCrumpetOpTags);
+    ops.def(
+        "fused_swin_attention_shifted(Tensor! out, Tensor q, Tensor k, Tensor v, Tensor bias, "
+        "int D, int H, int W, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w, "
+        "float scale) -> ()",
+        kCrumpetOpTags);
 }
 
 TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
@@ -228,4 +276,5 @@ TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
     ops.impl("fused_unshift_unpartition_3d", &fused_unshift_unpartition_3d);
     ops.impl("fused_unshift_unpartition_3d_backward", &fused_unshift_unpartition_3d_backward);
     ops.impl("fused_swin_attention", &fused_swin_attention);
+    ops.impl("fused_swin_attention_shifted", &fused_swin_attention_shifted);
 }

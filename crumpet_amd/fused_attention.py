@@ -83,4 +83,40 @@ def fused_swin_attention_windows(
     return out
 
 
-__all__ = ["fused_swin_attention"]
+def fused_swin_attention_shifted(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    relative_position_bias: torch.Tensor,
+    volume,
+    window_size,
+    shift_size,
+    scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Window attention with the shifted-window mask of a ``volume = (D, H, W)``.
+
+    Equivalent to ``fused_swin_attention(q, k, v, bias, mask, None, scale)``
+    with ``mask = compute_attn_mask_3d(D, H, W, window_size, shift_size)``
+    repeated over the outer batch (window ``b`` uses the mask of window
+    ``b % nW``), without materialising, repeating or reading the mask: the
+    kernel adds it from per-window-type bias+mask tables.  ``q``'s batch must
+    be a multiple of ``nW`` and ``N`` the window volume.
+    """
+    assert q.is_cuda and k.is_cuda and v.is_cuda
+    assert q.shape == k.shape == v.shape, "Q/K/V shape mismatch"
+    B, H, N, D = q.shape
+    assert relative_position_bias.shape == (H, N, N)
+    if scale is None:
+        scale = 1.0 / (D ** 0.5)
+    if out is None:
+        out = torch.empty_like(q)
+    Dv, Hv, Wv = (int(x) for x in volume)
+    ws = tuple(int(x) for x in window_size)
+    ss = tuple(int(x) for x in shift_size)
+    _native.ops().fused_swin_attention_shifted(
+        out, q, k, v, relative_position_bias, Dv, Hv, Wv, *ws, *ss, float(scale))
+    return out
+
+
+__all__ = ["fused_swin_attention", "fused_swin_attention_shifted"]

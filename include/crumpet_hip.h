@@ -173,7 +173,8 @@ CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  * workspace    : device buffer of at least
  *                crumpet_fused_swin_attention_workspace_size(Hh, N) bytes,
  *                16-byte aligned.  It holds the padded fp32 copy of the bias
- *                built at the start of the call.
+ *                built at the start of the call; calls that share a
+ *                workspace must be ordered on one stream.
  *
  * Supported: Dh = 16, 1 <= N <= 512.
  *
@@ -199,6 +200,40 @@ CRUMPET_API int crumpet_fused_swin_attention(void* out, const int64_t out_stride
 
 /* Bytes of workspace crumpet_fused_swin_attention needs for Hh heads and N tokens. */
 CRUMPET_API size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N);
+
+/*
+ * Fused window attention with the shifted-window mask of a [D, H, W] volume
+ * (window ws, shift ss) instead of a mask tensor.  Bit-identical in meaning
+ * to crumpet_fused_swin_attention with
+ *   mask = crumpet_compute_attn_mask_3d(D, H, W, ws, ss)   ([nW, N, N]),
+ *   mask_batch = nW, boundary = NULL,
+ * for B a multiple of nW = (D/ws_d)(H/ws_h)(W/ws_w) and N = ws_d*ws_h*ws_w:
+ * window b uses the mask of window b mod nW (the order MONAI tiles windows in).
+ * The mask is never materialised: the kernel adds it from per-window-type
+ * bias+mask tables built in the workspace, which must hold
+ * crumpet_fused_swin_attention_shifted_workspace_size(Hh, N) bytes.
+ *
+ * Has no dispatcher-op counterpart in the reference; it replaces the
+ * `mask.repeat` + `abs().amax` + masked Triton launch sequence of
+ * torch-ext/crumpet/monai_patch.py:167-191 for the patched MONAI path.
+ */
+CRUMPET_API int crumpet_fused_swin_attention_shifted(
+    void* out, const int64_t out_strides[4],
+    const void* q, const int64_t q_strides[4],
+    const void* k, const int64_t k_strides[4],
+    const void* v, const int64_t v_strides[4],
+    int32_t dtype,
+    int64_t B, int64_t Hh, int64_t N, int64_t Dh,
+    const void* bias, int32_t bias_dtype, const int64_t bias_strides[3],
+    int64_t D, int64_t H, int64_t W,
+    int64_t ws_d, int64_t ws_h, int64_t ws_w,
+    int64_t ss_d, int64_t ss_h, int64_t ss_w,
+    float scale,
+    void* workspace, size_t workspace_bytes,
+    void* stream);
+
+/* Bytes of workspace crumpet_fused_swin_attention_shifted needs. */
+CRUMPET_API size_t crumpet_fused_swin_attention_shifted_workspace_size(int64_t Hh, int64_t N);
 
 #ifdef __cplusplus
 } /* extern "C" */

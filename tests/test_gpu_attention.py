@@ -186,3 +186,73 @@ def test_config3_stage0_sampled(oracle, dev):
     ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), _f32(mask[sample]),
                            bnd.numpy()[sample], scale=0.25)
     _compare(out[torch.from_numpy(sample).to(dev)], ref, dtype, "config3 sample")
+
+
+SHIFTED_CASES = [
+    # (volume, window, shift, outer batch)
+    ((14, 14, 14), (7, 7, 7), (3, 3, 3), 2),
+    ((14, 7, 21), (7, 7, 7), (3, 0, 2), 1),
+    ((14, 14, 14), (7, 7, 7), (0, 0, 0), 1),
+    ((12, 12, 12), (6, 6, 6), (3, 3, 3), 1),
+    ((8, 8, 8), (4, 4, 4), (2, 2, 2), 3),
+    ((7, 7, 7), (7, 7, 7), (3, 3, 3), 4),
+]
+
+
+@pytest.mark.parametrize("case", SHIFTED_CASES)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_shifted_region_mask_matches_oracle(oracle, dev, case, dtype):
+    """fused_swin_attention_shifted == attention with the compute_attn_mask_3d mask
+    tiled over the outer batch (window b uses mask[b % nW])."""
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted
+
+    vol, ws, ss, outer = case
+    nW = (vol[0] // ws[0]) * (vol[1] // ws[1]) * (vol[2] // ws[2])
+    N = ws[0] * ws[1] * ws[2]
+    B, H, Dh = nW * outer, 3, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 1000 + N)
+    rows = (2 * ws[0] - 1) * (2 * ws[1] - 1) * (2 * ws[2] - 1)
+    bias = bias_from_table(trunc_normal_table(rows, H, 1001), ws).to(dtype)
+    m = oracle.attn_mask(*vol, ws, ss, "float32")
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m, None, scale=0.25)
+    out = fused_swin_attention_shifted(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), vol, ws, ss,
+                                       scale=0.25)
+    _compare(out, ref, dtype, f"shifted {case} {dtype}")
+
+
+def test_shifted_equals_tensor_mask_path(oracle, dev):
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted
+
+    dtype = torch.float16
+    vol, ws, ss = (14, 14, 14), (7, 7, 7), (3, 3, 3)
+    B, H, N, Dh = 16, 3, 343, 16
+    q, k, v = (t.to(dev) for t in _inputs(B, H, N, Dh, dtype, 1100))
+    bias = _bias(H, N, dtype, 1101).to(dev)
+    import crumpet_amd
+
+    mask = crumpet_amd.compute_attn_mask_3d(*vol, ws, ss, dtype, dev)
+    a = fused_swin_attention_shifted(q, k, v, bias, vol, ws, ss, scale=0.25)
+    b = torch.empty_like(q)
+    fused_swin_attention_windows(q, k, v, bias, mask, None, 0.25, b)
+    assert (a.float() - b.float()).abs().max().item() <= 1e-3
+
+
+def test_config3_stage0_shifted_sampled(oracle, dev):
+    """Config 3 through the region-mask path, sampled windows vs the oracle."""
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted
+
+    dtype = torch.float16
+    D, ws, ss = 49, (7, 7, 7), (3, 3, 3)
+    B, H, N, Dh = 1372, 3, 343, 16
+    qkv = seeded((B, N, 3 * H * Dh), dtype, 1200)
+    bias = bias_from_table(trunc_normal_table(2197, H, 1201), ws).to(dtype)
+    td = qkv.to(dev).reshape(B, N, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    out_bnc = torch.empty((B, N, H * Dh), dtype=dtype, device=dev)
+    out = out_bnc.view(B, N, H, Dh).permute(0, 2, 1, 3)
+    fused_swin_attention_shifted(td[0], td[1], td[2], bias.to(dev), (D, D, D), ws, ss, scale=0.25, out=out)
+    assert torch.isfinite(out).all()
+    m = oracle.attn_mask(D, D, D, ws, ss, "float32")
+    sample = np.unique(np.concatenate([np.arange(0, B, 41), np.arange(336, 343), np.arange(1365, 1372)]))
+    t = qkv[sample].reshape(len(sample), N, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), m[sample % 343], None, scale=0.25)
+    _compare(out[torch.from_numpy(sample).to(dev)], ref, dtype, "config3 shifted sample")

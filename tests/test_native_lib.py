@@ -63,6 +63,9 @@ def test_workspace_size_closed_form():
     assert lib.crumpet_fused_swin_attention_workspace_size(3, 343) == 3 * 352 * 352 * 4
     assert lib.crumpet_fused_swin_attention_workspace_size(24, 216) == 24 * 224 * 224 * 4
     assert lib.crumpet_fused_swin_attention_workspace_size(0, 343) == 0
+    lib.crumpet_fused_swin_attention_shifted_workspace_size.restype = ctypes.c_size_t
+    lib.crumpet_fused_swin_attention_shifted_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    assert lib.crumpet_fused_swin_attention_shifted_workspace_size(3, 343) == 8 * 3 * 352 * 352 * 4
 
 
 def test_host_argument_checks_need_no_gpu():
