@@ -186,6 +186,9 @@ def bench_attention(args, dev):
     mb = (mask.float()[idx % mask.shape[0]] * bnd[idx].float()[:, None, None])[:, None]
     ref = torch.softmax(s + mb, dim=-1) @ vf
     res["max_abs_err"] = float((ovs[0][idx].float() - ref).abs().max())
+    attn_shifted(0)
+    torch.cuda.synchronize()
+    res["max_abs_err_shifted"] = float((ovs[0][idx].float() - ref).abs().max())
     del qf, kf, vf, s, mb, ref
 
     if not args.no_eager:
@@ -231,12 +234,15 @@ def cpu_baseline():
 
 
 def profile_run(dev):
-    """Fixed short sequence for rocprofv3: 10 launches of each kernel plus a
-    plain 256 MiB device copy (read 256 MiB + write 256 MiB) for scaling the
-    FETCH_SIZE / WRITE_SIZE counters."""
+    """Fixed short sequence for rocprofv3: 20 launches of each kernel on
+    rotating buffers, plus a plain 256 MiB device copy (read 256 MiB + write
+    256 MiB) for scaling the FETCH_SIZE / WRITE_SIZE counters."""
     import torch
 
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
+
     ops = torch.ops.crumpet_ops
+    n = 20
     B, D, H, W, C, ws, ss = (C1[k] for k in ("B", "D", "H", "W", "C", "ws", "ss"))
     R = 4
     xs = [seeded((B, D, H, W, C), torch.float16, 100 + r).to(dev) for r in range(R)]
@@ -244,28 +250,47 @@ def profile_run(dev):
     backs = [torch.empty_like(xs[0]) for _ in range(R)]
     src = torch.ones((1 << 27,), dtype=torch.float16, device=dev)
     dst = torch.empty_like(src)
-    for i in range(10):
+    for i in range(n):
         ops.fused_shift_partition_3d(wins[i % R], xs[i % R], *ws, *ss)
-    for i in range(10):
+    for i in range(n):
         ops.fused_unshift_unpartition_3d(backs[i % R], wins[i % R], B, D, H, W, C, *ws, *ss)
-    out = torch.empty((2744, 343, 343), dtype=torch.float16, device=dev)
-    for i in range(10):
-        ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
+    del xs, wins, backs
+    outs = [torch.empty((2744, 343, 343), dtype=torch.float16, device=dev) for _ in range(2)]
+    for i in range(n):
+        ops.compute_attn_mask_3d(outs[i % 2], 98, 98, 98, 7, 7, 7, 3, 3, 3)
     for i in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
-    del out
-    from crumpet_amd.fused_attention import fused_swin_attention_windows
+    del outs
 
     qkvs, bias, mask, bnd = c3_inputs(dev, 3)
     Bw, Hh, N, Dh = C3["B"], C3["H"], C3["N"], C3["Dh"]
     o = torch.empty((Bw, N, Hh * Dh), dtype=torch.float16, device=dev)
     ov = o.view(Bw, N, Hh, Dh).permute(0, 2, 1, 3)
-    for i in range(10):
+    for i in range(n):
         t = qkvs[i % 3].reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4)
         fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ov)
     torch.cuda.synchronize()
+    vol = (C3["D"],) * 3
+    for i in range(n):
+        t = qkvs[i % 3].reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4)
+        fused_swin_attention_shifted(t[0], t[1], t[2], bias, vol, (7, 7, 7), (3, 3, 3), 0.25, ov)
+    torch.cuda.synchronize()
     print("profile sequence done", flush=True)
+
+
+def profiled_traffic(name):
+    """HBM bytes per launch of a kernel, as measured by the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (copy-calibrated), or None."""
+    path = ROOT / "profiles" / "window_gather_c1.md"
+    try:
+        for line in path.read_text().splitlines():
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "TRAFFIC" and parts[1] == name:
+                return int(parts[2])
+    except OSError:
+        return None
+    return None
 
 
 def main():
@@ -322,6 +347,7 @@ def main():
                   "frac_mfma_f16": round(tfl_s / MFMA_F16_PEAK_TFLOPS, 4),
                   "GB_s": round(C3_BYTES / (a["t_shift"] * 1e-3) / 1e9, 1),
                   "frac_hbm": round(C3_BYTES / (a["t_shift"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                  "max_abs_err_vs_fp32": a["max_abs_err_shifted"],
                   "workload": "config 3 through fused_swin_attention_shifted (mask from the 49^3 "
                               "geometry, never materialised)"}
         if "t_eager" in a:
@@ -346,7 +372,10 @@ def main():
                    "bytes_per_step": 2 * C1_BYTES, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs_part, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs_part / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel": "window_gather_kernel (shift-partition)",
+                     "traffic": profiled_traffic("partition"),
+                     "traffic_source": "profiles/window_gather_c1.md (rocprofv3 FETCH_SIZE/WRITE_SIZE, "
+                                       "copy-calibrated)",
+                     "kernel": "window_gather_kernel (shift-partition)",
                      "avg_launch_ms": round(p["t_part"], 5)},
         "components": components,
     }
