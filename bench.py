@@ -49,6 +49,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-attention", action="store_true")
     p.add_argument("--no-eager", action="store_true", help="skip the eager GPU attention chain")
+    p.add_argument("--no-blocks", action="store_true", help="skip the config-4 stage block paths")
+    p.add_argument("--no-e2e", action="store_true", help="skip the config-5 Swin UNETR forward")
     p.add_argument("--profile", action="store_true",
                    help="short fixed launch sequence for rocprofv3 (plus a copy of known size)")
     return p.parse_args()
@@ -210,6 +212,128 @@ def bench_attention(args, dev):
     return res
 
 
+STAGES = [  # config 4: (name, padded dim, C, heads, window, shift)
+    ("s1", 28, 96, 6, (7, 7, 7), (3, 3, 3)),
+    ("s2", 14, 192, 12, (7, 7, 7), (3, 3, 3)),
+    ("s3", 7, 384, 24, (7, 7, 7), (0, 0, 0)),
+    ("s3_monai", 6, 384, 24, (6, 6, 6), (0, 0, 0)),
+]
+
+
+def bench_blocks(args, dev):
+    """Config 4: partition -> fused attention -> unpartition per Swin stage, B=4.
+
+    The windows' C channels are read as H heads of 16 (q = k = v = the
+    partitioned tokens, so the timed chain is exactly the three hot-path
+    kernels; the qkv/proj linears are library GEMMs outside the path)."""
+    import torch
+
+    import crumpet_amd
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted
+
+    res = {}
+    for dtype, tag in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
+        for name, dim, C, H, ws, ss in STAGES:
+            B = 4
+            x = seeded((B, dim, dim, dim, C), dtype, 500 + dim).to(dev)
+            N = ws[0] * ws[1] * ws[2]
+            g = torch.Generator().manual_seed(510 + dim)
+            table = torch.empty(((2 * ws[0] - 1) * (2 * ws[1] - 1) * (2 * ws[2] - 1), H))
+            torch.nn.init.trunc_normal_(table, std=0.02, a=-2.0, b=2.0, generator=g)
+            import numpy as np
+
+            c = np.stack(np.meshgrid(*(np.arange(w) for w in ws), indexing="ij")).reshape(3, -1)
+            rel = c[:, :, None] - c[:, None, :] + np.array(ws)[:, None, None] - 1
+            rpi = torch.from_numpy((rel[0] * (2 * ws[1] - 1) + rel[1]) * (2 * ws[2] - 1) + rel[2])
+            bias = table[rpi.reshape(-1)].reshape(N, N, H).permute(2, 0, 1).contiguous().to(dtype).to(dev)
+
+            def step(i):
+                w = crumpet_amd.fused_shift_partition_3d(x, ws, ss)
+                nwin = w.shape[0]
+                t = w.view(nwin, N, H, 16).permute(0, 2, 1, 3)
+                o = torch.empty_like(w)
+                fused_swin_attention_shifted(t, t, t, bias, (dim,) * 3, ws, ss, 0.25,
+                                             o.view(nwin, N, H, 16).permute(0, 2, 1, 3))
+                crumpet_amd.fused_unshift_unpartition_3d(o, B, dim, dim, dim, C, ws, ss)
+
+            _events_time(step, args.warmup)
+            ms = _events_time(step, args.steps)
+            tokens = B * dim ** 3
+            part_bytes = 2 * tokens * C * x.element_size()
+            flops = 4 * N * N * 16 * H * (tokens // N)
+            res[f"{name}_{tag}"] = {"ms": round(ms, 5), "shape": [B, dim, dim, dim, C], "heads": H,
+                                    "window": list(ws), "shift": list(ss),
+                                    "partition_bytes": part_bytes, "attention_flops": flops,
+                                    "effective_GB_s": round(3 * part_bytes / (ms * 1e-3) / 1e9, 1)}
+            del x
+    return res
+
+
+def synthetic_ct(shape, seed):
+    """Config 5 input: uniform [0,1] intensities plus smooth Gaussian blobs, clamped to [0,1]."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    b, c, d, h, w = shape
+    vol = torch.rand(shape, generator=g) * 0.5
+    zz, yy, xx = torch.meshgrid(torch.arange(d), torch.arange(h), torch.arange(w), indexing="ij")
+    for _ in range(12):
+        ctr = torch.rand(3, generator=g) * torch.tensor([d, h, w])
+        sigma = 4.0 + 8.0 * torch.rand(1, generator=g).item()
+        amp = 0.3 + 0.5 * torch.rand(1, generator=g).item()
+        r2 = (zz - ctr[0]) ** 2 + (yy - ctr[1]) ** 2 + (xx - ctr[2]) ** 2
+        vol += amp * torch.exp(-r2 / (2 * sigma * sigma))
+    return vol.clamp_(0.0, 1.0)
+
+
+def bench_e2e(args, dev):
+    """Config 5: MONAI-style Swin UNETR forward, [4,1,96,96,96] fp16 input,
+    fp16 autocast, patched vs unpatched eager on the same weights."""
+    import statistics
+
+    import torch
+
+    import crumpet_amd
+    from crumpet_amd import swin_unetr_compat as sw
+
+    crumpet_amd.unpatch_monai_swin_unetr()
+    torch.manual_seed(123)
+    model = sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=48, depths=(2, 2, 2, 2),
+                         num_heads=(3, 6, 12, 24)).to(dev).eval()
+    x = synthetic_ct((4, 1, 96, 96, 96), 77).half().to(dev)
+
+    def timed(n):
+        times = []
+        y = None
+        with torch.no_grad():
+            for _ in range(n):
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                with torch.autocast("cuda", dtype=torch.float16):
+                    y = model(x)
+                e.record()
+                torch.cuda.synchronize()
+                times.append(s.elapsed_time(e))
+        return statistics.median(times), y
+
+    iters = max(3, min(10, args.steps // 10))
+    timed(2)
+    t_eager, y_eager = timed(iters)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    try:
+        timed(2)
+        t_patch, y_patch = timed(iters)
+    finally:
+        crumpet_amd.unpatch_monai_swin_unetr()
+    delta = float((y_patch.float() - y_eager.float()).abs().max())
+    return {"ms_patched": round(t_patch, 3), "ms_eager": round(t_eager, 3),
+            "speedup": round(t_eager / t_patch, 3), "max_abs_logit_delta": delta,
+            "max_abs_logit": float(y_eager.float().abs().max()), "iters": iters,
+            "workload": "config 5: SwinUNETR(1->14, feature 48, depths 2222, heads 3/6/12/24), "
+                        "input [4,1,96,96,96] fp16 (uniform + Gaussian blobs), fp16 autocast, "
+                        "median of iters forwards"}
+
+
 def cpu_baseline():
     """Oracle (C scalar, 1 thread) round trip on the full config-1 volume."""
     import numpy as np
@@ -316,6 +440,10 @@ def main():
     torch.cuda.empty_cache()
     a = {} if args.no_attention else bench_attention(args, dev)
     torch.cuda.empty_cache()
+    blocks = {} if args.no_blocks else bench_blocks(args, dev)
+    torch.cuda.empty_cache()
+    e2e = {} if args.no_e2e else bench_e2e(args, dev)
+    torch.cuda.empty_cache()
 
     gbs_step = 2 * C1_BYTES / (p["t_step"] * 1e-3) / 1e9
     gbs_part = C1_BYTES / (p["t_part"] * 1e-3) / 1e9
@@ -353,6 +481,10 @@ def main():
         if "t_eager" in a:
             comp_s["speedup_vs_eager"] = round(a["t_eager"] / a["t_shift"], 2)
         components["attention_shifted"] = comp_s
+    if blocks:
+        components["block_path"] = blocks
+    if e2e:
+        components["swin_unetr_e2e"] = e2e
 
     line = {
         "metric": "partition/unpartition GB/s (% HBM peak); window-attn TFLOP/s; ms per 96³ fwd",

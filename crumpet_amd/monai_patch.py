@@ -1,0 +1,218 @@
+"""Reversible patch of MONAI-style Swin UNETR models onto the gfx950 kernels.
+
+Same entry points and patched methods as torch-ext/crumpet/monai_patch.py:
+``patch_monai_swin_unetr()`` (idempotent; True when it installs the patch,
+False when already active) and ``unpatch_monai_swin_unetr()`` (restores
+the originals; True / False likewise) replace
+
+* ``SwinTransformerBlock.forward_part1``: norm1, pad to the window grid,
+  ``fused_shift_partition_3d``, window attention,
+  ``fused_unshift_unpartition_3d``, crop (reference :72-114);
+* ``BasicLayer.forward``: channels-last stage loop with the cached
+  ``compute_attn_mask_3d`` mask (reference :201-232);
+* ``WindowAttention.forward``: the eager ``q k^T + bias + mask -> softmax
+  -> @ v`` chain becomes one gfx950 kernel call (reference :117-198).  It
+  falls back to the original in training mode, with attention dropout,
+  when ``CRUMPET_DISABLE_FUSED_ATTN=1``, or for a head dimension other
+  than 16 (the kernel's only head dimension; every Swin UNETR stage has
+  16).
+
+Differences from the reference's patched attention, none of which changes
+the math:
+
+* q, k and v are passed to the kernel as strided views of the qkv linear's
+  output (no ``.contiguous()`` copies), and the kernel writes straight into
+  a ``[b, n, H, hd]`` buffer, so the ``transpose(1, 2).reshape`` copy
+  disappears;
+* in a shifted block whose mask came from the patched ``BasicLayer`` the
+  kernel derives the shifted-window mask from the window geometry
+  (``fused_swin_attention_shifted``): nothing is tiled with
+  ``mask.repeat`` and no mask or boundary flags are read.  Any other mask is
+  read as ``mask[b mod nW]`` with boundary flags computed on the ``nW``
+  distinct windows only;
+* the relative-position bias stays in the table's dtype (fp32), as in the
+  eager MONAI chain, instead of being rounded to the activation dtype.
+
+MONAI is optional: the patch applies to ``monai.networks.nets.swin_unetr``
+when it is importable, and always to ``crumpet_amd.swin_unetr_compat`` (the
+in-repo MONAI-compatible model used when MONAI is absent).
+"""
+
+from __future__ import annotations
+
+import functools
+import os
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+
+from . import compute_attn_mask_3d, fused_shift_partition_3d, fused_unshift_unpartition_3d
+from .fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
+
+_STATE: dict[str, Any] = {}
+_REQUIRED = ("SwinTransformerBlock", "BasicLayer", "WindowAttention", "get_window_size")
+# Attribute names: the mask geometry tag set by the patched BasicLayer, and the
+# per-call region handed from forward_part1 to the attention module.
+_GEOMETRY_ATTR = "_crumpet_geometry"
+_REGION_ATTR = "_crumpet_region"
+
+
+def _fused_attn_enabled() -> bool:
+    """Opt-out via ``CRUMPET_DISABLE_FUSED_ATTN=1`` (reference monai_patch.py:47-51)."""
+    return os.environ.get("CRUMPET_DISABLE_FUSED_ATTN", "0") != "1"
+
+
+def _swin_modules() -> list:
+    """Modules to patch: MONAI's swin_unetr if importable, plus the in-repo one."""
+    mods = []
+    try:
+        import monai.networks.nets.swin_unetr as monai_swin  # noqa: F401
+
+        if all(hasattr(monai_swin, n) for n in _REQUIRED):
+            mods.append(monai_swin)
+    except Exception:
+        pass
+    from . import swin_unetr_compat
+
+    mods.append(swin_unetr_compat)
+    return mods
+
+
+def _as_triple(value) -> tuple[int, int, int]:
+    if len(value) != 3:
+        raise RuntimeError("CRUMPET MONAI patch only supports 3D Swin blocks")
+    return tuple(int(v) for v in value)
+
+
+def _patched_forward_part1(original, swin):
+    @functools.wraps(original)
+    def forward_part1(self, x, mask_matrix):
+        if x.dim() != 5:
+            return original(self, x, mask_matrix)
+        x = self.norm1(x)
+        b, d, h, w, c = x.shape
+        window_size, shift_size = swin.get_window_size((d, h, w), self.window_size, self.shift_size)
+        window_size = _as_triple(window_size)
+        shift_size = _as_triple(shift_size)
+        pad_d1 = (window_size[0] - d % window_size[0]) % window_size[0]
+        pad_b = (window_size[1] - h % window_size[1]) % window_size[1]
+        pad_r = (window_size[2] - w % window_size[2]) % window_size[2]
+        if pad_d1 > 0 or pad_b > 0 or pad_r > 0:
+            x = F.pad(x, (0, 0, 0, pad_r, 0, pad_b, 0, pad_d1))
+        _, dp, hp, wp, _ = x.shape
+
+        shifted = any(s > 0 for s in shift_size)
+        attn_mask = mask_matrix if shifted else None
+        region = None
+        if shifted and getattr(mask_matrix, _GEOMETRY_ATTR, None) == (dp, hp, wp, window_size, shift_size):
+            region = ((dp, hp, wp), window_size, shift_size)
+
+        x_windows = fused_shift_partition_3d(x, window_size, shift_size)
+        setattr(self.attn, _REGION_ATTR, region)
+        try:
+            attn_windows = self.attn(x_windows, mask=attn_mask)
+        finally:
+            setattr(self.attn, _REGION_ATTR, None)
+        x = fused_unshift_unpartition_3d(attn_windows, B=b, D=dp, H=hp, W=wp, C=c,
+                                         window_size=window_size, shift_size=shift_size)
+        if pad_d1 > 0 or pad_r > 0 or pad_b > 0:
+            x = x[:, :d, :h, :w, :].contiguous()
+        return x
+
+    return forward_part1
+
+
+def _patched_window_attention_forward(original):
+    @functools.wraps(original)
+    def forward(self, x, mask):
+        if self.training or self.attn_drop.p != 0.0 or not _fused_attn_enabled():
+            return original(self, x, mask)
+        b, n, c = x.shape
+        heads = self.num_heads
+        hd = c // heads
+        if hd != 16 or hd * heads != c:
+            return original(self, x, mask)
+
+        qkv = self.qkv(x)  # [b, n, 3c]; channel = s*c + h*hd + d
+        t = qkv.view(b, n, 3, heads, hd).permute(2, 0, 3, 1, 4)  # views [b, H, n, hd]
+        idx = self.relative_position_index[:n, :n].reshape(-1)
+        bias = self.relative_position_bias_table[idx].view(n, n, heads).permute(2, 0, 1)
+        out = torch.empty((b, n, heads, hd), dtype=qkv.dtype, device=qkv.device)
+        ov = out.permute(0, 2, 1, 3)
+        region = getattr(self, _REGION_ATTR, None)
+        if mask is not None and region is not None:
+            volume, ws, ss = region
+            fused_swin_attention_shifted(t[0], t[1], t[2], bias, volume, ws, ss, self.scale, ov)
+        elif mask is not None:
+            nw = mask.shape[0]
+            flags = (mask.reshape(nw, -1).abs().amax(dim=1) > 0).to(torch.uint8)
+            boundary = flags.repeat(b // nw).contiguous()
+            fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, boundary, self.scale, ov)
+        else:
+            fused_swin_attention_windows(t[0], t[1], t[2], bias, None, None, self.scale, ov)
+        x = self.proj(out.view(b, n, c))
+        return self.proj_drop(x)
+
+    return forward
+
+
+def _patched_basic_layer_forward(original, swin):
+    @functools.wraps(original)
+    def forward(self, x):
+        if x.dim() != 5:
+            return original(self, x)
+        b, c, d, h, w = x.shape
+        window_size, shift_size = swin.get_window_size((d, h, w), self.window_size, self.shift_size)
+        window_size = _as_triple(window_size)
+        shift_size = _as_triple(shift_size)
+        x = x.permute(0, 2, 3, 4, 1).contiguous()
+        dp = -(-d // window_size[0]) * window_size[0]
+        hp = -(-h // window_size[1]) * window_size[1]
+        wp = -(-w // window_size[2]) * window_size[2]
+        attn_mask = compute_attn_mask_3d(D=dp, H=hp, W=wp, window_size=window_size,
+                                         shift_size=shift_size, dtype=x.dtype, device=x.device)
+        setattr(attn_mask, _GEOMETRY_ATTR, (dp, hp, wp, window_size, shift_size))
+        for blk in self.blocks:
+            x = blk(x, attn_mask)
+        x = x.view(b, d, h, w, -1)
+        if self.downsample is not None:
+            x = self.downsample(x)
+        return x.permute(0, 4, 1, 2, 3).contiguous()
+
+    return forward
+
+
+def patch_monai_swin_unetr() -> bool:
+    """Install the patch.  Returns True on the call that installs it and False
+    if it is already active (reference monai_patch.py:235-261)."""
+    if _STATE.get("patched"):
+        return False
+    saved = []
+    for swin in _swin_modules():
+        orig = (swin.SwinTransformerBlock.forward_part1, swin.BasicLayer.forward,
+                swin.WindowAttention.forward)
+        saved.append((swin, orig))
+        swin.SwinTransformerBlock.forward_part1 = _patched_forward_part1(orig[0], swin)
+        swin.BasicLayer.forward = _patched_basic_layer_forward(orig[1], swin)
+        if _fused_attn_enabled():
+            swin.WindowAttention.forward = _patched_window_attention_forward(orig[2])
+    _STATE.update({"patched": True, "saved": saved})
+    return True
+
+
+def unpatch_monai_swin_unetr() -> bool:
+    """Restore the original methods.  Returns True if a patch was removed
+    (reference monai_patch.py:264-275)."""
+    if not _STATE.get("patched"):
+        return False
+    for swin, orig in _STATE["saved"]:
+        swin.SwinTransformerBlock.forward_part1 = orig[0]
+        swin.BasicLayer.forward = orig[1]
+        swin.WindowAttention.forward = orig[2]
+    _STATE.clear()
+    return True
+
+
+def is_patched() -> bool:
+    return bool(_STATE.get("patched"))

@@ -1,0 +1,133 @@
+"""GPU parity of the patched MONAI-style Swin UNETR with its own eager forward.
+
+The reference pins its patch only by idempotence (tests/test_monai_patch.py)
+and by a hd=4 demo that bypasses fused attention
+(tests/test_demo_btcv_smoke.py:37-39).  Here the patched forwards
+(partition / attention / unpartition kernels, both attention mask modes)
+are compared with the unpatched eager forwards of the same modules and
+weights, at the Swin UNETR stage shapes (window 7, shift 3, padding to the
+window grid, the 6^3 stage with window 6 and no shift):
+
+* fp32: the kernels compute in fp32, so the patched block matches eager to
+  1e-4 (absolute, activations of order 1);
+* fp16 autocast: eager rounds the scores to fp16 before adding the bias,
+  the kernel keeps them in fp32, so the bound is 1e-2 relative to the
+  largest activation.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import crumpet_amd
+from crumpet_amd import monai_patch
+from crumpet_amd import swin_unetr_compat as sw
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def patched():
+    crumpet_amd.unpatch_monai_swin_unetr()
+    yield
+    crumpet_amd.unpatch_monai_swin_unetr()
+
+
+def _run(module, *args, autocast=False):
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+        return module(*args)
+
+
+def _layer(dim, heads, seed, depth=2):
+    torch.manual_seed(seed)
+    return sw.BasicLayer(dim=dim, depth=depth, num_heads=heads, window_size=(7, 7, 7), drop_path=0.0,
+                         qkv_bias=True, downsample=None)
+
+
+@pytest.mark.parametrize("dims,dim,heads", [((12, 12, 12), 48, 3),   # padded to 14^3, shifted
+                                            ((14, 14, 14), 96, 6),   # no padding, shifted
+                                            ((6, 6, 6), 384, 24)])   # window 6, no shift (N=216)
+def test_patched_basic_layer_matches_eager_fp32(patched, dev, dims, dim, heads):
+    layer = _layer(dim, heads, 0).to(dev).eval()
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn((2, dim) + dims, generator=g).to(dev)
+    want = _run(layer, x)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(layer, x)
+    err = (got - want).abs().max().item()
+    print(f"basic layer {dims} C={dim}: max-abs {err:.2e}", flush=True)
+    assert err < 1e-4
+
+
+def test_patched_basic_layer_fp16_autocast(patched, dev):
+    layer = _layer(48, 3, 2).to(dev).eval()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((2, 48, 12, 12, 12), generator=g).to(dev)
+    want = _run(layer, x, autocast=True).float()
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(layer, x, autocast=True).float()
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    print(f"fp16 autocast: max-abs {err:.2e} (max |x| {scale:.2f})", flush=True)
+    assert err < 1e-2 * scale
+
+
+def test_region_mode_reads_no_mask(patched, dev, monkeypatch):
+    """A shifted block under the patched BasicLayer takes the geometry path."""
+    calls = []
+    real = monai_patch.fused_swin_attention_windows
+
+    def spy(q, k, v, bias, mask, boundary, scale, out):
+        calls.append(mask is not None)
+        return real(q, k, v, bias, mask, boundary, scale, out)
+
+    monkeypatch.setattr(monai_patch, "fused_swin_attention_windows", spy)
+    layer = _layer(48, 3, 4).to(dev).eval()
+    x = torch.randn((1, 48, 14, 14, 14), device=dev)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    _run(layer, x)
+    assert calls == [False]  # block 0 (no shift) only; block 1 used the shifted entry point
+
+
+def test_block_with_foreign_mask_uses_tensor_mask(patched, dev):
+    """A mask that did not come from the patched BasicLayer is read as a tensor (mask[b mod nW])."""
+    torch.manual_seed(5)
+    blk = sw.SwinTransformerBlock(dim=48, num_heads=3, window_size=(7, 7, 7), shift_size=(3, 3, 3)).to(dev).eval()
+    x = torch.randn((3, 14, 14, 14, 48), device=dev)
+    mask = sw.compute_mask((14, 14, 14), (7, 7, 7), (3, 3, 3), dev)
+    want = _run(blk, x, mask)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(blk, x, mask)
+    err = (got - want).abs().max().item()
+    print(f"foreign mask: max-abs {err:.2e}", flush=True)
+    assert err < 1e-4
+
+
+def test_patched_swin_unetr_matches_eager_fp32(patched, dev):
+    torch.manual_seed(7)
+    model = sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=48).to(dev).eval()
+    g = torch.Generator().manual_seed(8)
+    x = torch.rand((1, 1, 64, 64, 64), generator=g).to(dev)
+    want = _run(model, x)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(model, x)
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    print(f"SwinUNETR 64^3 fp32: max-abs logit delta {err:.2e} (max |logit| {scale:.2f})", flush=True)
+    assert err < 1e-4 * max(1.0, scale)
+
+
+def test_training_mode_falls_back_and_backpropagates(patched, dev):
+    torch.manual_seed(9)
+    layer = _layer(48, 3, 9, depth=2).to(dev).train()
+    x = torch.randn((1, 48, 14, 14, 14), device=dev, requires_grad=True)
+    want = layer(x)
+    want.square().mean().backward()
+    g_want = x.grad.clone()
+    x.grad = None
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = layer(x)
+    got.square().mean().backward()
+    assert (got - want).abs().max().item() < 1e-4
+    assert (x.grad - g_want).abs().max().item() < 1e-5
