@@ -28,9 +28,7 @@ C_ABI_SYMBOLS = (
     "crumpet_unshift_unpartition_3d_backward",
     "crumpet_compute_attn_mask_3d",
     "crumpet_fused_swin_attention",
-    "crumpet_fused_swin_attention_workspace_size",
     "crumpet_fused_swin_attention_shifted",
-    "crumpet_fused_swin_attention_shifted_workspace_size",
 )
 
 OP_NAMES = (

@@ -1,8 +1,8 @@
-// Host side of the fused window attention: argument checks, the fp32 bias
-// (+ shifted-window mask) tables in the workspace, the window-type table of
-// the region mode, the work decomposition, and dispatch to the per-dtype
-// kernel instantiations (attention_f16.hip, attention_bf16.hip,
-// attention_f32.hip; the kernel itself is in attention_kernel.h).
+// Host side of the fused window attention: argument checks, the window-type
+// table of the region mode, the work decomposition, and dispatch to the
+// per-dtype kernel instantiations (attention_f16.hip, attention_bf16.hip,
+// attention_f32.hip; the kernel itself is in attention_kernel.h).  Nothing
+// here allocates: the kernel builds its bias tiles from the bias tensor.
 //
 // Replaces the Triton launch of torch-ext/crumpet/fused_attention.py:149-226.
 #include <hip/hip_runtime.h>
@@ -16,53 +16,8 @@
 namespace crumpet {
 namespace {
 
-constexpr int kPrepThreads = 256;
 // Workgroups a call aims for: each walks win_per_wg windows; ~4 per CU.
 constexpr int64_t kTargetWorkgroups = 1024;
-
-// Local-coordinate class of a window token for the shifted-window mask:
-// one bit per axis, set when the coordinate lies at or past ws - ss.
-struct RegionCls {
-    int32_t ws_d, ws_h, ws_w, ss_d, ss_h, ss_w;
-    __device__ __forceinline__ int cls(int loc) const {
-        const int lw = loc % ws_w;
-        const int t = loc / ws_w;
-        const int lh = t % ws_h;
-        const int ld = t / ws_h;
-        return ((ld >= ws_d - ss_d) ? 4 : 0) | ((lh >= ws_h - ss_h) ? 2 : 0) |
-               ((lw >= ws_w - ss_w) ? 1 : 0);
-    }
-};
-
-// tables[c][h][i][j] (c < ntables): bias[h][i][j], plus -100 where the
-// shifted-window mask of window type code c separates tokens i and j
-// (region mode only); -inf in padded key columns, 0 in padded query rows.
-template <typename TB>
-__global__ void __launch_bounds__(kPrepThreads)
-table_prep_kernel(float* __restrict__ ws, const TB* __restrict__ bias, int64_t sh, int64_t si,
-                  int64_t sj, int32_t H, int32_t N, int32_t NP, int32_t ntables, int32_t region,
-                  RegionCls rc) {
-    const int64_t total = int64_t(ntables) * H * NP * NP;
-    for (int64_t idx = int64_t(blockIdx.x) * kPrepThreads + threadIdx.x; idx < total;
-         idx += int64_t(gridDim.x) * kPrepThreads) {
-        const int32_t j = static_cast<int32_t>(idx % NP);
-        int64_t r = idx / NP;
-        const int32_t i = static_cast<int32_t>(r % NP);
-        r /= NP;
-        const int32_t h = static_cast<int32_t>(r % H);
-        const int32_t code = static_cast<int32_t>(r / H);
-        float val;
-        if (j >= N) {
-            val = -INFINITY;
-        } else if (i >= N) {
-            val = 0.0f;
-        } else {
-            val = static_cast<float>(bias[h * sh + i * si + j * sj]);
-            if (region && ((rc.cls(i) ^ rc.cls(j)) & code)) val += -100.0f;
-        }
-        ws[idx] = val;
-    }
-}
 
 int dtype_size(int32_t dt) {
     switch (dt) {
@@ -71,14 +26,6 @@ int dtype_size(int32_t dt) {
         case CRUMPET_DTYPE_BF16: return 2;
         default: return 0;
     }
-}
-
-size_t table_bytes(int64_t Hh, int64_t N, int ntables) {
-    if (Hh <= 0 || N <= 0) return 0;
-    const int nt = attn::select_tiles(N);
-    if (nt < 0) return 0;
-    const int64_t np = 16 * nt;
-    return static_cast<size_t>(ntables * Hh * np * np * int64_t(sizeof(float)));
 }
 
 struct Region {
@@ -93,8 +40,7 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                   int64_t N, int64_t Dh, const void* bias, int32_t bias_dtype,
                   const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
                   int64_t mask_batch, const int64_t mask_strides[3], const uint8_t* boundary,
-                  const Region* region, float scale, void* workspace, size_t workspace_bytes,
-                  void* stream) {
+                  const Region* region, float scale, void* stream) {
     const int esize = dtype_size(dtype);
     if (esize == 0) return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported dtype %d", what, dtype);
     if (B < 0 || Hh < 0 || N < 0 || Dh <= 0)
@@ -113,6 +59,11 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: null pointer argument", what);
     if (dtype_size(bias_dtype) == 0)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported bias dtype %d", what, bias_dtype);
+    if (bias_strides[2] != 1 || bias_strides[0] < 0 || bias_strides[1] < 0)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                    "%s: bias must have unit stride along keys", what);
+    if (((N - 1) * bias_strides[1] + N) * dtype_size(bias_dtype) >= (int64_t(1) << 31))
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: bias row stride out of range", what);
     if (mask != nullptr) {
         if (dtype_size(mask_dtype) == 0)
             return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported mask dtype %d", what,
@@ -132,8 +83,10 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     }
 
     attn::Params p = {};
-    RegionCls rc = {1, 1, 1, 0, 0, 0};
-    int ntables = 1;
+    for (int a = 0; a < 3; ++a) {
+        p.ws[a] = 1;
+        p.ss[a] = 0;
+    }
     if (region != nullptr) {
         const Region& rg = *region;
         for (int a = 0; a < 3; ++a) {
@@ -181,19 +134,13 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         }
         p.types.ntypes = nt;
         p.types.offset[nt] = static_cast<int32_t>(off);
-        rc = {int32_t(rg.ws[0]), int32_t(rg.ws[1]), int32_t(rg.ws[2]),
-              int32_t(rg.ss[0]), int32_t(rg.ss[1]), int32_t(rg.ss[2])};
-        ntables = 8;
+        for (int a = 0; a < 3; ++a) {
+            p.ws[a] = static_cast<int32_t>(rg.ws[a]);
+            p.ss[a] = static_cast<int32_t>(rg.ss[a]);
+        }
     }
 
-    const size_t need = table_bytes(Hh, N, ntables);
-    if (workspace == nullptr || workspace_bytes < need ||
-        reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
-        return fail(CRUMPET_ERR_INVALID_ARGUMENT,
-                    "%s: workspace must be 16-byte aligned and hold %zu bytes", what, need);
-
     const int NT = attn::select_tiles(N);
-    const int NP = 16 * NT;
     p.q = q;
     p.k = k;
     p.v = v;
@@ -204,7 +151,9 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         p.vs[i] = v_strides[i];
         p.os[i] = out_strides[i];
     }
-    p.table = static_cast<const float*>(workspace);
+    p.bias = bias;
+    for (int i = 0; i < 3; ++i) p.bsd[i] = bias_strides[i];
+    p.bias_dtype = bias_dtype;
     p.mask = mask;
     for (int i = 0; i < 3; ++i) p.ms[i] = mask ? mask_strides[i] : 0;
     p.mask_batch = mask ? static_cast<int32_t>(mask_batch) : 1;
@@ -238,27 +187,6 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.vec_io = vec ? 1 : 0;
 
     hipStream_t s = static_cast<hipStream_t>(stream);
-    {
-        const int64_t total = int64_t(ntables) * Hh * NP * NP;
-        int64_t blocks = (total + kPrepThreads - 1) / kPrepThreads;
-        if (blocks > 8192) blocks = 8192;
-        float* ws = static_cast<float*>(workspace);
-        const int32_t reg = region != nullptr ? 1 : 0;
-        if (bias_dtype == CRUMPET_DTYPE_F16)
-            hipLaunchKernelGGL(table_prep_kernel<_Float16>, dim3(blocks), dim3(kPrepThreads), 0, s,
-                               ws, static_cast<const _Float16*>(bias), bias_strides[0],
-                               bias_strides[1], bias_strides[2], p.H, p.N, NP, ntables, reg, rc);
-        else if (bias_dtype == CRUMPET_DTYPE_BF16)
-            hipLaunchKernelGGL(table_prep_kernel<__bf16>, dim3(blocks), dim3(kPrepThreads), 0, s,
-                               ws, static_cast<const __bf16*>(bias), bias_strides[0],
-                               bias_strides[1], bias_strides[2], p.H, p.N, NP, ntables, reg, rc);
-        else
-            hipLaunchKernelGGL(table_prep_kernel<float>, dim3(blocks), dim3(kPrepThreads), 0, s,
-                               ws, static_cast<const float*>(bias), bias_strides[0],
-                               bias_strides[1], bias_strides[2], p.H, p.N, NP, ntables, reg, rc);
-        const int st2 = check_launch(what);
-        if (st2 != CRUMPET_OK) return st2;
-    }
     const int kmask = region != nullptr                  ? attn::kMaskRegion
                       : mask == nullptr                  ? attn::kNoMask
                       : mask_dtype == CRUMPET_DTYPE_F32  ? attn::kMaskF32
@@ -276,26 +204,17 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
 }  // namespace
 }  // namespace crumpet
 
-extern "C" size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N) {
-    return crumpet::table_bytes(Hh, N, 1);
-}
-
-extern "C" size_t crumpet_fused_swin_attention_shifted_workspace_size(int64_t Hh, int64_t N) {
-    return crumpet::table_bytes(Hh, N, 8);
-}
-
 extern "C" int crumpet_fused_swin_attention(
     void* out, const int64_t out_strides[4], const void* q, const int64_t q_strides[4],
     const void* k, const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
     int32_t dtype, int64_t B, int64_t Hh, int64_t N, int64_t Dh, const void* bias,
     int32_t bias_dtype, const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
     int64_t mask_batch, const int64_t mask_strides[3], const uint8_t* boundary, float scale,
-    void* workspace, size_t workspace_bytes, void* stream) {
+    void* stream) {
     return crumpet::run_attention("crumpet_fused_swin_attention", out, out_strides, q, q_strides,
                                   k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
                                   bias_dtype, bias_strides, mask, mask_dtype, mask_batch,
-                                  mask_strides, boundary, nullptr, scale, workspace,
-                                  workspace_bytes, stream);
+                                  mask_strides, boundary, nullptr, scale, stream);
 }
 
 extern "C" int crumpet_fused_swin_attention_shifted(
@@ -304,10 +223,10 @@ extern "C" int crumpet_fused_swin_attention_shifted(
     int32_t dtype, int64_t B, int64_t Hh, int64_t N, int64_t Dh, const void* bias,
     int32_t bias_dtype, const int64_t bias_strides[3], int64_t D, int64_t H, int64_t W,
     int64_t ws_d, int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w,
-    float scale, void* workspace, size_t workspace_bytes, void* stream) {
+    float scale, void* stream) {
     const crumpet::Region rg = {D, H, W, {ws_d, ws_h, ws_w}, {ss_d, ss_h, ss_w}};
     return crumpet::run_attention("crumpet_fused_swin_attention_shifted", out, out_strides, q,
                                   q_strides, k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
                                   bias_dtype, bias_strides, nullptr, 0, 1, nullptr, nullptr, &rg,
-                                  scale, workspace, workspace_bytes, stream);
+                                  scale, stream);
 }

@@ -12,10 +12,11 @@
 //   The relative-position bias is the same for every window, so it is kept in
 //   registers instead of being re-read per window: a workgroup of 4 waves
 //   owns one head h and a group of 4 consecutive 16-query strips, and walks a
-//   contiguous range of windows.  Each wave loads the fp32 bias tiles of its
-//   strip (NT tiles of 16 keys x 16 queries, 4 values per lane each) once and
-//   uses them as the accumulator input of every window's S^T = K Q^T MFMAs,
-//   so the bias add costs neither memory traffic nor VALU work.
+//   contiguous range of windows.  Each wave builds the fp32 bias tiles of its
+//   strip (NT tiles of 16 keys x 16 queries, 4 values per lane each) once,
+//   straight from the caller's bias tensor (any float dtype and strides),
+//   and uses them as the accumulator input of every window's S^T = K Q^T
+//   MFMAs, so the bias add costs neither memory traffic nor VALU work.
 //
 //   Q (the group's 64 rows, pre-scaled and rounded), K (row-major) and V
 //   (transposed) of a window live in LDS, double-buffered: while the waves
@@ -24,8 +25,8 @@
 //
 //   In region mode the windows are visited grouped by type (which axes the
 //   window is last on; at most 8 types).  The shifted-window mask of a window
-//   depends only on its type, so the host prepares bias+mask tables per type
-//   and a type change is just a register reload - the mask costs nothing per
+//   depends only on its type, so it is folded into the bias tiles when the
+//   type changes (at most 8 times per workgroup) and costs nothing per
 //   window.  Logical index -> window uses per-type offsets and mixed-radix
 //   decoding (Params::types).
 //
@@ -40,9 +41,9 @@
 //   lane, which is one 8-byte store.
 //
 // Padding
-//   Workspace tables are [T][H][NP][NP] fp32 (NP = 16*NT); padded key
-//   columns hold -inf (probability exactly 0), padded query rows 0.  K, V and
-//   Q rows past N are zero in LDS.
+//   Keys are padded to NP = 16*NT: padded key columns get a -inf bias
+//   (probability exactly 0), padded query rows a 0 bias (never stored).  K, V
+//   and Q rows past N are zero in LDS.  The kernel needs no workspace.
 //
 // Numerics follow torch-ext/crumpet/fused_attention.py:82-146: q is scaled
 // in fp32 and rounded back to the input type, products accumulate in fp32,
@@ -83,7 +84,9 @@ struct Params {
     const void* v;
     void* out;
     int64_t qs[4], ks[4], vs[4], os[4];  // element strides (b, h, n, d)
-    const float* table;                  // [T][H][NP][NP] fp32 bias (+ mask per type)
+    const void* bias;                    // [H][N][N], element strides bsd (bsd[2] == 1)
+    int64_t bsd[3];
+    int32_t bias_dtype;                  // crumpet_dtype code
     const void* mask;                    // tensor mode: [M][N][N], unit key stride
     int64_t ms[3];
     int32_t mask_batch;
@@ -98,6 +101,7 @@ struct Params {
     uint32_t chunks, launched;
     // region mode geometry
     int32_t nWd, nWh, nWw, nW;  // windows per volume along D, H, W and in total
+    int32_t ws[3], ss[3];       // window and shift sizes
     TypeTable types;
 };
 
@@ -281,11 +285,84 @@ struct Stage {
     }
 };
 
-// Bias (+ region mask) tiles of one strip: rows qi of the table, 4 keys per lane per tile.
-template <int NT>
-__device__ __forceinline__ void load_tiles(f32x4 (&bs)[NT], const float* row) {
+// A workgroup-uniform 64-bit address made provably uniform (scalar
+// registers).  readfirstlane returns a signed int: both halves are taken as
+// uint32_t so that the low word is zero-extended, not sign-extended.
+__device__ __forceinline__ char* uniform_ptr(const void* ptr) {
+    const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
+    return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// Bias (+ region mask) tiles of one strip, built in registers from the
+// caller's bias tensor: lane (col, g) holds keys 16t + 4g + r of query qi.
+// The head's [N, N] bias is read through a buffer descriptor, so every load
+// is one instruction with an immediate offset; keys past N read 0 or the
+// next row and are replaced by -inf (probability exactly 0).  Padded query
+// rows get 0 (never stored).  In region mode a key whose shift-region class
+// differs from the query's on an axis that the window type `code` splits
+// gets -100.  Runs when the window type changes (at most 8 times per
+// workgroup), never per window.
+template <int NT, int kMask>
+__device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, int h, int qi, int g,
+                                            int code, const uint8_t* cls) {
+    // Re-read the kernel arguments (Params is the kernel's only argument, at
+    // offset 0 of the kernarg segment) through an opaque copy of the segment
+    // pointer, so that the compiler loads them here instead of keeping them
+    // live in scalar registers across the whole window loop.
+    (void)prm;
+    typedef const __attribute__((address_space(4))) Params KParams;
+    KParams* pp = (KParams*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(pp));
+    const int N = pp->N;
+    const int bias_dtype = pp->bias_dtype;
+    const int64_t bsd0 = pp->bsd[0], bsd1 = pp->bsd[1];
+    const void* bias_ptr = pp->bias;
+    const bool row = qi < N;
+    const int qr = row ? qi : N - 1;
+    const int es = bias_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
+    const bool bf16 = bias_dtype == CRUMPET_DTYPE_BF16;
+    // base and extent are workgroup-uniform; readfirstlane keeps the
+    // descriptor in SGPRs (a VGPR descriptor costs a waterfall loop per load)
+    char* hb = uniform_ptr(static_cast<const char*>(bias_ptr) + int64_t(h) * bsd0 * es);
+    const int extent =
+        __builtin_amdgcn_readfirstlane(static_cast<int>((int64_t(N - 1) * bsd1 + N) * es));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(hb, 0, extent, 0x00020000);
+    const int voff = static_cast<int>((int64_t(qr) * bsd1 + 4 * g) * es);
+    uint32_t cq = 0, cmask = 0;
+    if constexpr (kMask == kMaskRegion) {
+        cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
+        cmask = uint32_t(code) * 0x01010101u;
+    }
 #pragma unroll
-    for (int t = 0; t < NT; ++t) bs[t] = *reinterpret_cast<const f32x4*>(row + 16 * t);
+    for (int t = 0; t < NT; ++t) {
+        uint32_t split = 0;  // byte r nonzero: key 16t+4g+r is masked by the region rule
+        if constexpr (kMask == kMaskRegion)
+            split = (*reinterpret_cast<const uint32_t*>(&cls[16 * t + 4 * g]) ^ cq) & cmask;
+        float v4[4];
+        if (es == 4) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                v4[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, voff + (16 * t + r) * 4, 0, 0));
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + (16 * t + r) * 2, 0, 0);
+                const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+                v4[r] = bf16 ? __uint_as_float(bits << 16) : fh;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            float val = v4[r];
+            if constexpr (kMask == kMaskRegion) {
+                if ((split >> (8 * r)) & 0xffu) val += -100.0f;
+            }
+            val = row ? val : 0.0f;
+            bs[t][r] = (16 * t + 4 * g + r) < N ? val : -INFINITY;
+        }
+    }
 }
 
 // One strip (16 queries, NT*16 keys) of one window.
@@ -311,10 +388,12 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
     uint32_t mq[kUseMask ? 4 * kPrefetch : 1];
     if constexpr (kUseMask) {
         const int qr = qi < N ? qi : N - 1;
-        const char* mbase = static_cast<const char*>(p.mask) +
-                            int64_t(b % p.mask_batch) * p.ms[0] * kMaskBytes;
-        const int extent = static_cast<int>(((N - 1) * p.ms[1] + N) * kMaskBytes);
-        mrsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(mbase), 0, extent, 0x00020000);
+        // uniform base and extent, kept in scalar registers (see build_tiles)
+        char* mb = uniform_ptr(static_cast<const char*>(p.mask) +
+                               int64_t(b % p.mask_batch) * p.ms[0] * kMaskBytes);
+        const int extent =
+            __builtin_amdgcn_readfirstlane(static_cast<int>(((N - 1) * p.ms[1] + N) * kMaskBytes));
+        mrsrc = __builtin_amdgcn_make_buffer_rsrc(mb, 0, extent, 0x00020000);
         mvoff = static_cast<int>((qr * p.ms[1] + 4 * g) * kMaskBytes);
     }
     auto fetch = [&](int t, int slot) {
@@ -502,6 +581,7 @@ swin_attention_d16_kernel(const Params p) {
     __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * 16];
     __shared__ __attribute__((aligned(16))) T k_lds[2][NP * 16];
     __shared__ __attribute__((aligned(16))) T vt_lds[2][16 * St::kVtStride];
+    __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
 
     uint32_t chunk;
     if (!xcd_chunk(blockIdx.x, p.launched, p.chunks, chunk)) return;
@@ -523,9 +603,22 @@ swin_attention_d16_kernel(const Params p) {
     const bool active = strip < p.strips;
     const int q0 = grp * kWaves * 16;  // first query row of this group
 
-    // this wave's table row: [type][h][qi][4g ...]
-    const size_t type_stride = size_t(p.H) * NP * NP;
-    const float* trow = p.table + (size_t(h) * NP + (active ? qi : 0)) * NP + 4 * g;
+    if constexpr (kMask == kMaskRegion) {
+        // shift-region class of every window token: one bit per axis, set at
+        // or past ws - ss (covered by the prologue barrier below)
+        for (int j = threadIdx.x; j < NP; j += kThreads) {
+            int c = 0;
+            if (j < p.N) {
+                const int lw = j % p.ws[2];
+                const int t = j / p.ws[2];
+                const int lh = t % p.ws[1];
+                const int ld = t / p.ws[1];
+                c = ((ld >= p.ws[0] - p.ss[0]) ? 4 : 0) | ((lh >= p.ws[1] - p.ss[1]) ? 2 : 0) |
+                    ((lw >= p.ws[2] - p.ss[2]) ? 1 : 0);
+            }
+            cls_lds[j] = static_cast<uint8_t>(c);
+        }
+    }
 
     St st;
     int code_cur = -1;
@@ -546,7 +639,7 @@ swin_attention_d16_kernel(const Params p) {
         }
         if (active) {
             if (code != code_cur) {  // workgroup-uniform: new bias (+ mask) tiles
-                load_tiles<NT>(bs, trow + (kMask == kMaskRegion ? code * type_stride : 0));
+                build_tiles<NT, kMask>(bs, p, h, qi, g, code, cls_lds);
                 code_cur = code;
             }
             bool use_mask = false;

@@ -177,9 +177,6 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
     }
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
     if (out.numel() == 0) return;
-    const size_t ws_bytes = crumpet_fused_swin_attention_workspace_size(Hh, N);
-    at::Tensor ws = at::empty({static_cast<int64_t>((ws_bytes + 15) / 16) * 4},
-                              q.options().dtype(at::kFloat));
     int64_t qs[4], ks[4], vs[4], os[4], bs[3];
     for (int i = 0; i < 4; ++i) {
         qs[i] = q.stride(i);
@@ -187,11 +184,13 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
         vs[i] = v.stride(i);
         os[i] = out.stride(i);
     }
-    for (int i = 0; i < 3; ++i) bs[i] = bias.stride(i);
+    // the kernel reads bias rows through unit key stride
+    const at::Tensor bk = bias.stride(2) == 1 ? bias : bias.contiguous();
+    for (int i = 0; i < 3; ++i) bs[i] = bk.stride(i);
     check_status(crumpet_fused_swin_attention(
         out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
-        bias.data_ptr(), bdt, bs, mptr, mdt, mbatch, ms, bptr, static_cast<float>(scale),
-        ws.data_ptr(), ws_bytes, stream_of(q)));
+        bk.data_ptr(), bdt, bs, mptr, mdt, mbatch, ms, bptr, static_cast<float>(scale),
+        stream_of(q)));
 }
 
 void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
@@ -218,9 +217,6 @@ void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at
     TORCH_CHECK(bdt >= 0, what, ": bias dtype must be float32, float16 or bfloat16");
     const c10::hip::HIPGuardMasqueradingAsCUDA guard(dev);
     if (out.numel() == 0) return;
-    const size_t ws_bytes = crumpet_fused_swin_attention_shifted_workspace_size(Hh, N);
-    at::Tensor ws = at::empty({static_cast<int64_t>((ws_bytes + 15) / 16) * 4},
-                              q.options().dtype(at::kFloat));
     int64_t qs[4], ks[4], vs[4], os[4], bs[3];
     for (int i = 0; i < 4; ++i) {
         qs[i] = q.stride(i);
@@ -228,11 +224,12 @@ void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at
         vs[i] = v.stride(i);
         os[i] = out.stride(i);
     }
-    for (int i = 0; i < 3; ++i) bs[i] = bias.stride(i);
+    const at::Tensor bk = bias.stride(2) == 1 ? bias : bias.contiguous();
+    for (int i = 0; i < 3; ++i) bs[i] = bk.stride(i);
     check_status(crumpet_fused_swin_attention_shifted(
         out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
-        bias.data_ptr(), bdt, bs, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w,
-        static_cast<float>(scale), ws.data_ptr(), ws_bytes, stream_of(q)));
+        bk.data_ptr(), bdt, bs, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w,
+        static_cast<float>(scale), stream_of(q)));
 }
 
 }  // namespace

@@ -137,7 +137,8 @@ def _patched_window_attention_forward(original):
         qkv = self.qkv(x)  # [b, n, 3c]; channel = s*c + h*hd + d
         t = qkv.view(b, n, 3, heads, hd).permute(2, 0, 3, 1, 4)  # views [b, H, n, hd]
         idx = self.relative_position_index[:n, :n].reshape(-1)
-        bias = self.relative_position_bias_table[idx].view(n, n, heads).permute(2, 0, 1)
+        # gather from the transposed table: [H, n*n], unit stride along keys
+        bias = self.relative_position_bias_table.t()[:, idx].view(heads, n, n)
         out = torch.empty((b, n, heads, hd), dtype=qkv.dtype, device=qkv.device)
         ov = out.permute(0, 2, 1, 3)
         region = getattr(self, _REGION_ATTR, None)

@@ -161,7 +161,8 @@ CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  *
  * q, k, v, out : [B, Hh, N, Dh] with arbitrary element strides (in elements,
  *                order b, h, n, d); dtype F16, BF16 or F32 (all four equal).
- * bias         : [Hh, N, N], strides (h, i, j), dtype F32/F16/BF16.
+ * bias         : [Hh, N, N], strides (h, i, j) with unit j stride, dtype
+ *                F32/F16/BF16.
  * mask         : [mask_batch, N, N] or NULL; strides (m, i, j) with unit j
  *                stride; mask_batch
  *                must divide B (1 broadcasts, B is per window, nW repeats
@@ -170,11 +171,8 @@ CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  *                reads its mask; a zero flag skips the mask for that window.
  * scale        : softmax scale; q is multiplied by it in fp32 and rounded
  *                back to the input type before the product.
- * workspace    : device buffer of at least
- *                crumpet_fused_swin_attention_workspace_size(Hh, N) bytes,
- *                16-byte aligned.  It holds the padded fp32 copy of the bias
- *                built at the start of the call; calls that share a
- *                workspace must be ordered on one stream.
+ *
+ * Needs no workspace: every buffer is an input or the output.
  *
  * Supported: Dh = 16, 1 <= N <= 512.
  *
@@ -195,11 +193,7 @@ CRUMPET_API int crumpet_fused_swin_attention(void* out, const int64_t out_stride
                                  const int64_t mask_strides[3],
                                  const uint8_t* boundary,
                                  float scale,
-                                 void* workspace, size_t workspace_bytes,
                                  void* stream);
-
-/* Bytes of workspace crumpet_fused_swin_attention needs for Hh heads and N tokens. */
-CRUMPET_API size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64_t N);
 
 /*
  * Fused window attention with the shifted-window mask of a [D, H, W] volume
@@ -209,9 +203,9 @@ CRUMPET_API size_t crumpet_fused_swin_attention_workspace_size(int64_t Hh, int64
  *   mask_batch = nW, boundary = NULL,
  * for B a multiple of nW = (D/ws_d)(H/ws_h)(W/ws_w) and N = ws_d*ws_h*ws_w:
  * window b uses the mask of window b mod nW (the order MONAI tiles windows in).
- * The mask is never materialised: the kernel adds it from per-window-type
- * bias+mask tables built in the workspace, which must hold
- * crumpet_fused_swin_attention_shifted_workspace_size(Hh, N) bytes.
+ * The mask is never materialised or read: windows are processed grouped by
+ * their boundary type and the kernel folds the type's mask into its bias
+ * tiles.  Needs no workspace.
  *
  * Has no dispatcher-op counterpart in the reference; it replaces the
  * `mask.repeat` + `abs().amax` + masked Triton launch sequence of
@@ -229,11 +223,7 @@ CRUMPET_API int crumpet_fused_swin_attention_shifted(
     int64_t ws_d, int64_t ws_h, int64_t ws_w,
     int64_t ss_d, int64_t ss_h, int64_t ss_w,
     float scale,
-    void* workspace, size_t workspace_bytes,
     void* stream);
-
-/* Bytes of workspace crumpet_fused_swin_attention_shifted needs. */
-CRUMPET_API size_t crumpet_fused_swin_attention_shifted_workspace_size(int64_t Hh, int64_t N);
 
 #ifdef __cplusplus
 } /* extern "C" */

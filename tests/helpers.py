@@ -72,11 +72,12 @@ def c_abi():
     lib.crumpet_fused_swin_attention.restype = ctypes.c_int
     lib.crumpet_fused_swin_attention.argtypes = [
         vp, p4, vp, p4, vp, p4, vp, p4, ctypes.c_int32, i64, i64, i64, i64,
-        vp, ctypes.c_int32, p4, vp, ctypes.c_int32, i64, p4, vp, ctypes.c_float,
-        vp, ctypes.c_size_t, vp,
+        vp, ctypes.c_int32, p4, vp, ctypes.c_int32, i64, p4, vp, ctypes.c_float, vp,
     ]
-    lib.crumpet_fused_swin_attention_workspace_size.restype = ctypes.c_size_t
-    lib.crumpet_fused_swin_attention_workspace_size.argtypes = [i64, i64]
+    lib.crumpet_fused_swin_attention_shifted.restype = ctypes.c_int
+    lib.crumpet_fused_swin_attention_shifted.argtypes = [
+        vp, p4, vp, p4, vp, p4, vp, p4, ctypes.c_int32, i64, i64, i64, i64,
+        vp, ctypes.c_int32, p4] + [i64] * 9 + [ctypes.c_float, vp]
     lib.crumpet_last_error.restype = ctypes.c_char_p
     lib.crumpet_status_string.restype = ctypes.c_char_p
     lib.crumpet_status_string.argtypes = [ctypes.c_int]

@@ -64,20 +64,28 @@ def test_c_abi_attention(oracle, dev):
     mask = torch.from_numpy(oracle.attn_mask(14, 14, 14, (7, 7, 7), (3, 3, 3), "float16"))
     qd, kd, vd, bd, md = (t.to(dev) for t in (q, k, v, bias, mask))
     out = torch.empty_like(qd)
-    wsb = lib.crumpet_fused_swin_attention_workspace_size(H, N)
-    assert wsb == H * 352 * 352 * 4
-    ws = torch.empty((wsb // 4,), dtype=torch.float32, device=dev)
     st = lib.crumpet_fused_swin_attention(
         out.data_ptr(), strides(out, 4), qd.data_ptr(), strides(qd, 4), kd.data_ptr(), strides(kd, 4),
         vd.data_ptr(), strides(vd, 4), CODE[torch.float16], B, H, N, Dh,
         bd.data_ptr(), CODE[torch.float16], strides(bd, 3),
         md.data_ptr(), CODE[torch.float16], 8, strides(md, 3), None, ctypes.c_float(0.25),
-        ws.data_ptr(), wsb, _stream())
+        _stream())
     assert st == 0, lib.crumpet_last_error()
     torch.cuda.synchronize()
     ref = oracle.attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), bias.float().numpy(),
                            mask.float().numpy(), None, scale=0.25)
     assert np.abs(out.float().cpu().numpy() - ref).max() <= 2e-3
+
+    # the same windows through the geometry entry point (mask derived from the 14^3 volume)
+    out2 = torch.empty_like(qd)
+    st = lib.crumpet_fused_swin_attention_shifted(
+        out2.data_ptr(), strides(out2, 4), qd.data_ptr(), strides(qd, 4), kd.data_ptr(), strides(kd, 4),
+        vd.data_ptr(), strides(vd, 4), CODE[torch.float16], B, H, N, Dh,
+        bd.data_ptr(), CODE[torch.float16], strides(bd, 3), 14, 14, 14, 7, 7, 7, 3, 3, 3,
+        ctypes.c_float(0.25), _stream())
+    assert st == 0, lib.crumpet_last_error()
+    torch.cuda.synchronize()
+    assert np.abs(out2.float().cpu().numpy() - ref).max() <= 2e-3
 
 
 def test_c_abi_rejects_bad_arguments(dev):

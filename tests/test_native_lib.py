@@ -58,16 +58,6 @@ def test_version_and_status_strings():
     assert lib.crumpet_status_string(3) == b"CRUMPET_ERR_HIP"
 
 
-def test_workspace_size_closed_form():
-    lib = c_abi()
-    assert lib.crumpet_fused_swin_attention_workspace_size(3, 343) == 3 * 352 * 352 * 4
-    assert lib.crumpet_fused_swin_attention_workspace_size(24, 216) == 24 * 224 * 224 * 4
-    assert lib.crumpet_fused_swin_attention_workspace_size(0, 343) == 0
-    lib.crumpet_fused_swin_attention_shifted_workspace_size.restype = ctypes.c_size_t
-    lib.crumpet_fused_swin_attention_shifted_workspace_size.argtypes = [ctypes.c_int64, ctypes.c_int64]
-    assert lib.crumpet_fused_swin_attention_shifted_workspace_size(3, 343) == 8 * 3 * 352 * 352 * 4
-
-
 def test_host_argument_checks_need_no_gpu():
     """Invalid arguments are rejected before any HIP call."""
     lib = c_abi()
@@ -92,17 +82,26 @@ def test_attention_argument_checks_need_no_gpu():
     s3 = (ctypes.c_int64 * 3)(1, 1, 1)
     fake = ctypes.c_void_p(256)
 
-    def call(dtype=1, B=2, H=3, N=343, Dh=16, mask=None, mb=1, ws=fake, wsb=1 << 30):
+    def call(dtype=1, B=2, H=3, N=343, Dh=16, mask=None, mb=1):
         return lib.crumpet_fused_swin_attention(
             fake, s4, fake, s4, fake, s4, fake, s4, dtype, B, H, N, Dh, fake, 1, s3,
-            mask, 1, mb, s3, None, ctypes.c_float(0.25), ws, wsb, None)
+            mask, 1, mb, s3, None, ctypes.c_float(0.25), None)
 
     assert call(Dh=8) == 2
     assert call(N=600) == 2
     assert call(dtype=5) == 1
     assert call(mask=fake, mb=3) == 1  # mask batch must divide B
-    assert call(wsb=16) == 1  # workspace too small
     assert call(B=0) == 0
+
+    def shifted(B=8, N=343, D=14, ws=7, ss=3):
+        return lib.crumpet_fused_swin_attention_shifted(
+            fake, s4, fake, s4, fake, s4, fake, s4, 1, B, 3, N, 16, fake, 1, s3,
+            D, D, D, ws, ws, ws, ss, ss, ss, ctypes.c_float(0.25), None)
+
+    assert shifted(D=15) == 1 and b"divisible" in lib.crumpet_last_error()
+    assert shifted(ss=7) == 1 and b"shift" in lib.crumpet_last_error()
+    assert shifted(N=216) == 1 and b"window volume" in lib.crumpet_last_error()
+    assert shifted(B=6) == 1 and b"multiple" in lib.crumpet_last_error()
 
 
 def test_dispatcher_schemas_match_reference():
