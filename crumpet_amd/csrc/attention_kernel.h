@@ -195,31 +195,83 @@ constexpr int waves_per_eu() {
     return NT <= 4 ? 4 : (NT <= 8 ? 3 : 2);
 }
 
-// Logical window index -> window index b (region mode visits windows by type).
+// Walks the logical window indices [i0, i1) of a workgroup.  In region mode
+// windows are visited grouped by type: logical index -> (type t, outer batch,
+// window choice per axis) in mixed radix.  The start is decoded once; each
+// step is a carry chain of scalar compares (no divisions per window).
 template <int kMask>
-__device__ __forceinline__ int window_of(const Params& p, int i, int& type_code) {
-    if constexpr (kMask != kMaskRegion) {
-        type_code = 0;
-        return i;
-    } else {
-        int t = 0;
-        while (t + 1 < p.types.ntypes && i >= p.types.offset[t + 1]) ++t;
-        const int code = p.types.code[t];
-        const int cd = p.types.choices[t][0], ch = p.types.choices[t][1], cw = p.types.choices[t][2];
-        int j = i - p.types.offset[t];
-        const int per = cd * ch * cw;
-        const int batch = j / per;
-        j -= batch * per;
-        const int jw = j % cw;
-        j /= cw;
-        const int jh = j % ch;
-        const int jd = j / ch;
-        const int wd = (code & 4) ? p.nWd - 1 : jd;
-        const int wh = (code & 2) ? p.nWh - 1 : jh;
-        const int ww = (code & 1) ? p.nWw - 1 : jw;
-        type_code = code;
-        return batch * p.nW + (wd * p.nWh + wh) * p.nWw + ww;
+struct WindowIter {
+    int i;
+    int t, batch, jd, jh, jw;  // region mode position
+    int cd, ch, cw, code;      // choices of the current type, its code
+    int batches;               // outer batches (B / nW)
+
+    __device__ __forceinline__ void load_type(const Params& p) {
+        code = p.types.code[t];
+        cd = p.types.choices[t][0];
+        ch = p.types.choices[t][1];
+        cw = p.types.choices[t][2];
     }
+
+    __device__ __forceinline__ void init(const Params& p, int i0) {
+        i = i0;
+        if constexpr (kMask == kMaskRegion) {
+            batches = p.B / p.nW;
+            t = 0;
+            while (t + 1 < p.types.ntypes && i0 >= p.types.offset[t + 1]) ++t;
+            load_type(p);
+            int j = i0 - p.types.offset[t];
+            const int per = cd * ch * cw;
+            batch = j / per;
+            j -= batch * per;
+            jw = j % cw;
+            j /= cw;
+            jh = j % ch;
+            jd = j / ch;
+        }
+    }
+
+    // window index b of the current position; type_code of its mask
+    __device__ __forceinline__ int window(const Params& p, int& type_code) const {
+        if constexpr (kMask != kMaskRegion) {
+            type_code = 0;
+            return i;
+        } else {
+            const int wd = (code & 4) ? p.nWd - 1 : jd;
+            const int wh = (code & 2) ? p.nWh - 1 : jh;
+            const int ww = (code & 1) ? p.nWw - 1 : jw;
+            type_code = code;
+            return batch * p.nW + (wd * p.nWh + wh) * p.nWw + ww;
+        }
+    }
+
+    __device__ __forceinline__ void next(const Params& p) {
+        ++i;
+        if constexpr (kMask == kMaskRegion) {
+            if (++jw < cw) return;
+            jw = 0;
+            if (++jh < ch) return;
+            jh = 0;
+            if (++jd < cd) return;
+            jd = 0;
+            if (++batch < batches) return;
+            batch = 0;
+            if (t + 1 < p.types.ntypes) {
+                ++t;
+                load_type(p);
+            }
+        }
+    }
+};
+
+// A workgroup-uniform 64-bit address made provably uniform (scalar
+// registers).  readfirstlane returns a signed int: both halves are taken as
+// uint32_t so that the low word is zero-extended, not sign-extended.
+__device__ __forceinline__ char* uniform_ptr(const void* ptr) {
+    const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
+    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
+    return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
 // Staging of one window's Q (this group's rows), K and V into LDS.  Each
@@ -232,6 +284,7 @@ struct Stage {
     static constexpr int kQChunks = kQRows * 4;
     static constexpr int kChunks = kQChunks + 2 * NP * 4;
     static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
+    static constexpr int kRows = NP;           // K / V rows held in LDS
     static constexpr int kVtStride = NP + 4;  // keeps 8/16-byte rows, breaks bank aliasing
     typedef typename Frag<T>::x4 X4;
 
@@ -285,15 +338,73 @@ struct Stage {
     }
 };
 
-// A workgroup-uniform 64-bit address made provably uniform (scalar
-// registers).  readfirstlane returns a signed int: both halves are taken as
-// uint32_t so that the low word is zero-extended, not sign-extended.
-__device__ __forceinline__ char* uniform_ptr(const void* ptr) {
-    const uint64_t a = reinterpret_cast<uint64_t>(ptr);
-    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
-    const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
-    return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
+// Staging for rows with unit d stride and 4-element alignment (the MONAI
+// qkv layout).  Thread tid owns 4 dims (4*(tid&3)..) of rows tid/4 + 64k:
+// one Q row of this group and kKC rows each of K and V.  Loads go through
+// per-window buffer descriptors with 32-bit offsets; row indices past N are
+// clamped to N-1, which is harmless: padded keys have a -inf bias, padded V
+// rows meet P = 0 and padded query rows are never stored.  No branches and
+// no 64-bit address arithmetic per row.
+template <typename T, int NT>
+struct Stage<T, NT, true> {
+    static constexpr int NP = NT * 16;
+    static constexpr int kQRows = 16 * kWaves;
+    static constexpr int kKC = (NP + 63) / 64;  // K (and V) rows per thread
+    static constexpr int kRows = kKC * 64;       // K / V rows held in LDS (>= NP)
+    static constexpr int kVtStride = kRows + 4;
+    typedef typename Frag<T>::x4 X4;
+
+    X4 rq, rk[kKC], rv[kKC];
+
+    static __device__ __forceinline__ X4 ld(__amdgpu_buffer_rsrc_t rs, int off) {
+        if constexpr (sizeof(X4) == 8)
+            return __builtin_bit_cast(X4, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+        else
+            return __builtin_bit_cast(X4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+    }
+
+    static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t off,
+                                                                 int64_t s2, int N) {
+        char* ub = uniform_ptr(static_cast<const char*>(base) + off * int64_t(sizeof(T)));
+        const int extent = __builtin_amdgcn_readfirstlane(
+            static_cast<int>((int64_t(N - 1) * s2 + 16) * int64_t(sizeof(T))));
+        return __builtin_amdgcn_make_buffer_rsrc(ub, 0, extent, 0x00020000);
+    }
+
+    __device__ __forceinline__ void load(const Params& p, int b, int h, int q0) {
+        const int N = p.N;
+        const int n0 = threadIdx.x >> 2;
+        const int d0 = (threadIdx.x & 3) * 4;
+        const auto qr = rsrc(p.q, int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1], p.qs[2], N);
+        const auto kr = rsrc(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
+        const auto vr = rsrc(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
+        const int qs2 = static_cast<int>(p.qs[2]), ks2 = static_cast<int>(p.ks[2]),
+                  vs2 = static_cast<int>(p.vs[2]);
+        constexpr int es = sizeof(T);
+        const int nq = min(q0 + n0, N - 1);
+        rq = ld(qr, (nq * qs2 + d0) * es);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rq[e] = T(static_cast<float>(rq[e]) * p.scale);
+#pragma unroll
+        for (int k = 0; k < kKC; ++k) {
+            const int n = min(n0 + 64 * k, N - 1);
+            rk[k] = ld(kr, (n * ks2 + d0) * es);
+            rv[k] = ld(vr, (n * vs2 + d0) * es);
+        }
+    }
+
+    __device__ __forceinline__ void store(T* q_lds, T* k_lds, T* vt_lds) const {
+        const int tid = threadIdx.x;
+        const int n0 = tid >> 2, d0 = (tid & 3) * 4;
+        *reinterpret_cast<X4*>(&q_lds[tid * 4]) = rq;
+#pragma unroll
+        for (int k = 0; k < kKC; ++k) {
+            *reinterpret_cast<X4*>(&k_lds[(tid + k * kThreads) * 4]) = rk[k];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n0 + 64 * k] = rv[k][e];
+        }
+    }
+};
 
 // Bias (+ region mask) tiles of one strip, built in registers from the
 // caller's bias tensor: lane (col, g) holds keys 16t + 4g + r of query qi.
@@ -579,7 +690,7 @@ swin_attention_d16_kernel(const Params p) {
     typedef Stage<T, NT, kVec> St;
     constexpr int NP = St::NP;
     __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * 16];
-    __shared__ __attribute__((aligned(16))) T k_lds[2][NP * 16];
+    __shared__ __attribute__((aligned(16))) T k_lds[2][St::kRows * 16];
     __shared__ __attribute__((aligned(16))) T vt_lds[2][16 * St::kVtStride];
     __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
 
@@ -621,9 +732,11 @@ swin_attention_d16_kernel(const Params p) {
     }
 
     St st;
+    WindowIter<kMask> it;
+    it.init(p, i0);
     int code_cur = -1;
     int code_next;
-    int b_next = window_of<kMask>(p, i0, code_next);
+    int b_next = it.window(p, code_next);
     st.load(p, b_next, h, q0);
     st.store(q_lds[0], k_lds[0], vt_lds[0]);
     __syncthreads();
@@ -634,7 +747,8 @@ swin_attention_d16_kernel(const Params p) {
         const int b = b_next;
         const int code = code_next;
         if (i + 1 < i1) {
-            b_next = window_of<kMask>(p, i + 1, code_next);
+            it.next(p);
+            b_next = it.window(p, code_next);
             st.load(p, b_next, h, q0);
         }
         if (active) {
