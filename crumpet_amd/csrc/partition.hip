@@ -9,9 +9,10 @@
 // Index math uses FastDiv (one mulhi + add + shift per division), so the
 // VALU cost is ~50 instructions per 16-byte vector, a third of the VALU
 // budget at HBM speed.  One vector per thread with non-temporal stores and
-// the hardware's own workgroup order measured fastest on MI355X (5.68 TB/s
-// for the 98^3 C=48 fp16 partition, 96% of a plain streaming copy); more
-// vectors per thread or an XCD-contiguous remap were slower.
+// the hardware's own workgroup order measured fastest on MI355X for the
+// window-ordered direction (5.8 TB/s for the 98^3 C=48 fp16 partition, 98%
+// of a plain streaming copy); more vectors per thread were slower.  The
+// volume-ordered direction groups workgroups in runs per XCD (3-4% faster).
 //
 // Reference semantics: torch-ext/crumpet/reference.py:141-184 (roll then
 // view/permute, and the inverse); kernels replaced:
@@ -25,6 +26,7 @@ namespace crumpet {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr uint32_t kXcdRun = 32;  // workgroups per XCD run in the volume-ordered gather
 
 struct GatherGeom {
     uint32_t total;  // output vectors
@@ -106,7 +108,21 @@ __global__ void __launch_bounds__(kThreads)
 window_gather_kernel(typename VecOf<VB>::type* __restrict__ out,
                      const typename VecOf<VB>::type* __restrict__ in, const GatherGeom g) {
     typedef typename VecOf<VB>::type V;
-    const uint32_t base = blockIdx.x * (kThreads * U) + threadIdx.x;
+    uint32_t blk = blockIdx.x;
+    if constexpr (!kToWindows) {
+        // Volume-ordered output: consecutive rows read the two halves of the
+        // partial cache lines at the ends of each window row.  Give each XCD
+        // runs of kXcdRun consecutive workgroups (hardware ids go round-robin
+        // over the XCDs) so those rows share one L2; the tail keeps the
+        // identity mapping.
+        constexpr uint32_t kSpan = kNumXcd * kXcdRun;
+        const uint32_t sup = blk / kSpan;
+        if ((sup + 1) * kSpan <= gridDim.x) {
+            const uint32_t within = blk - sup * kSpan;
+            blk = sup * kSpan + (within % kNumXcd) * kXcdRun + within / kNumXcd;
+        }
+    }
+    const uint32_t base = blk * (kThreads * U) + threadIdx.x;
     V vals[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
