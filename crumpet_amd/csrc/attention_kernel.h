@@ -274,6 +274,24 @@ __device__ __forceinline__ char* uniform_ptr(const void* ptr) {
     return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// 2-byte element types keep V row-major in LDS (like K) and read the
+// V^T MFMA fragments with the gfx950 LDS transpose read: within each group
+// of 16 lanes, lane j receives element j%4 of the 8-byte vectors addressed by
+// lanes 4e + j/4 (e = 0..3).  Lane (col, g) addressing V row 16t + 4g + col/4
+// at dims 4*(col%4) therefore receives V[16t + 4g + e][col], e = 0..3.  fp32
+// keeps a transposed V (no 32-bit transpose read is used).
+template <typename T>
+constexpr bool v_row_major() {
+    return sizeof(T) == 2;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::x4 lds_read_tr(const T* ptr) {
+    typedef __attribute__((address_space(3))) i16x4 LdsI16x4;
+    const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((LdsI16x4*)(const_cast<T*>(ptr)));
+    return __builtin_bit_cast(typename Frag<T>::x4, r);
+}
+
 // Staging of one window's Q (this group's rows), K and V into LDS.  Each
 // thread owns chunks c = tid + k * kThreads of 4 elements; kQChunks Q chunks
 // come first, then NP*4 K chunks, then NP*4 V chunks.
@@ -329,9 +347,13 @@ struct Stage {
                     *reinterpret_cast<X4*>(&k_lds[cc * 4]) = r[k];
                 } else {
                     const int c2 = cc - NP * 4;
-                    const int n = c2 >> 2, d0 = (c2 & 3) * 4;
+                    if constexpr (v_row_major<T>()) {
+                        *reinterpret_cast<X4*>(&vt_lds[c2 * 4]) = r[k];
+                    } else {
+                        const int n = c2 >> 2, d0 = (c2 & 3) * 4;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n] = r[k][e];
+                        for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n] = r[k][e];
+                    }
                 }
             }
         }
@@ -400,8 +422,12 @@ struct Stage<T, NT, true> {
 #pragma unroll
         for (int k = 0; k < kKC; ++k) {
             *reinterpret_cast<X4*>(&k_lds[(tid + k * kThreads) * 4]) = rk[k];
+            if constexpr (v_row_major<T>()) {
+                *reinterpret_cast<X4*>(&vt_lds[(tid + k * kThreads) * 4]) = rv[k];
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n0 + 64 * k] = rv[k][e];
+                for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n0 + 64 * k] = rv[k][e];
+            }
         }
     }
 };
@@ -533,7 +559,9 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
     f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
     float lsum = 0.0f;  // fp32 path row sum (VALU)
     float m_run = -INFINITY;
-    const T* vrow = &vt_lds[col * kVtStride + 4 * g];
+    // V^T fragments: transposed layout (fp32) or transpose reads of row-major V
+    const T* vrow = v_row_major<T>() ? &vt_lds[(4 * g + (col >> 2)) * 16 + (col & 3) * 4]
+                                     : &vt_lds[col * kVtStride + 4 * g];
 
 #pragma unroll
     for (int c0 = 0; c0 < NT; c0 += kChunk) {
@@ -618,8 +646,8 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
                 if (u + 1 >= cn) break;
                 const int t = c0 + u;
                 X8 pb, va;
-                const X4 v0 = *reinterpret_cast<const X4*>(vrow + 16 * t);
-                const X4 v1 = *reinterpret_cast<const X4*>(vrow + 16 * t + 16);
+                const X4 v0 = lds_read_tr<T>(vrow + 256 * t);
+                const X4 v1 = lds_read_tr<T>(vrow + 256 * (t + 1));
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     pb[r] = T(S[u][r]);
@@ -635,7 +663,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
                 // half, so each accumulator chain uses a single MFMA opcode
                 const int u = cn - 1;
                 X8 pb, va;
-                const X4 v0 = *reinterpret_cast<const X4*>(vrow + 16 * (c0 + u));
+                const X4 v0 = lds_read_tr<T>(vrow + 256 * (c0 + u));
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     pb[r] = T(S[u][r]);
