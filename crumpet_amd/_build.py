@@ -46,6 +46,8 @@ HIPCC_FLAGS = [
     # packed fp32 VALU ops stay disabled on these boxes
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-command-line-argument",
+    # dma16() (attention_kernel.h) sets m0 in inline asm on purpose
+    "-Wno-inline-asm",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]

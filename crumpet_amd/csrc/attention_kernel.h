@@ -18,10 +18,14 @@
 //   and uses them as the accumulator input of every window's S^T = K Q^T
 //   MFMAs, so the bias add costs neither memory traffic nor VALU work.
 //
-//   Q (the group's 64 rows, pre-scaled and rounded), K (row-major) and V
-//   (transposed) of a window live in LDS, double-buffered: while the waves
-//   compute window i, each thread holds its share of window i+1 in registers
-//   and writes it to the other buffer afterwards; one barrier per window.
+//   Q (the group's 64 rows, pre-scaled and rounded), K and V of a window
+//   live in LDS, double-buffered, one barrier per window.  While the waves
+//   compute window i, window i+1 is fetched into the other buffer: for 2-byte
+//   types with unit d stride, K and V rows go straight from memory to LDS
+//   (buffer loads with the lds flag) and only Q passes through registers;
+//   otherwise each thread holds its share in registers and stores it after
+//   the compute (fp32 keeps V transposed; 2-byte types keep V row-major and
+//   read V^T with the LDS transpose read).
 //
 //   In region mode the windows are visited grouped by type (which axes the
 //   window is last on; at most 8 types).  The shifted-window mask of a window
@@ -304,11 +308,12 @@ struct Stage {
     static constexpr int kPerThread = (kChunks + kThreads - 1) / kThreads;
     static constexpr int kRows = NP;           // K / V rows held in LDS
     static constexpr int kVtStride = NP + 4;  // keeps 8/16-byte rows, breaks bank aliasing
+    static constexpr int kVLds = v_row_major<T>() ? kRows * 16 : 16 * kVtStride;
     typedef typename Frag<T>::x4 X4;
 
     X4 r[kPerThread];
 
-    __device__ __forceinline__ void load(const Params& p, int b, int h, int q0) {
+    __device__ __forceinline__ void load(const Params& p, int b, int h, int q0, T*, T*) {
         const T* qb = static_cast<const T*>(p.q) + b * p.qs[0] + h * p.qs[1];
         const T* kb = static_cast<const T*>(p.k) + b * p.ks[0] + h * p.ks[1];
         const T* vb = static_cast<const T*>(p.v) + b * p.vs[0] + h * p.vs[1];
@@ -367,16 +372,48 @@ struct Stage {
 // clamped to N-1, which is harmless: padded keys have a -inf bias, padded V
 // rows meet P = 0 and padded query rows are never stored.  No branches and
 // no 64-bit address arithmetic per row.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor words (base, stride 0, num_records, dword-3 flags) for a
+// window's rows, workgroup-uniform.
+template <typename T>
+__device__ __forceinline__ u32x4 desc_words(const void* base, int64_t off, int64_t s2, int N) {
+    const char* ub = uniform_ptr(static_cast<const char*>(base) + off * int64_t(sizeof(T)));
+    const uint64_t a = reinterpret_cast<uint64_t>(ub);
+    u32x4 d;
+    d[0] = static_cast<uint32_t>(a);
+    d[1] = static_cast<uint32_t>(a >> 32) & 0xffffu;
+    d[2] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
+        static_cast<int>((int64_t(N - 1) * s2 + 16) * int64_t(sizeof(T)))));
+    d[3] = 0x00020000u;
+    return d;
+}
+
+// 16 bytes per lane from buffer offset voff straight into LDS at
+// lds_addr + 16 * lane (lds_addr wave-uniform).  Written as inline asm so
+// that the compiler does not treat it as an LDS store it must wait for
+// before unrelated LDS reads; the caller waits (vmcnt(0)) before the barrier
+// that publishes the rows.
+__device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, int voff) {
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voff), "s"(desc)
+                 : "memory", "m0");
+}
+
 template <typename T, int NT>
 struct Stage<T, NT, true> {
     static constexpr int NP = NT * 16;
     static constexpr int kQRows = 16 * kWaves;
-    static constexpr int kKC = (NP + 63) / 64;  // K (and V) rows per thread
-    static constexpr int kRows = kKC * 64;       // K / V rows held in LDS (>= NP)
+    static constexpr bool kDma = v_row_major<T>();
+    static constexpr int kKC = (NP + 63) / 64;          // register path: rows per thread
+    static constexpr int kRows = kDma ? (NP + 31) / 32 * 32 : kKC * 64;
+    static constexpr int kRounds = (kRows + 127) / 128;  // DMA path: 32-row loads per wave
     static constexpr int kVtStride = kRows + 4;
+    static constexpr int kVLds = v_row_major<T>() ? kRows * 16 : 16 * kVtStride;
     typedef typename Frag<T>::x4 X4;
 
-    X4 rq, rk[kKC], rv[kKC];
+    X4 rq, rk[kDma ? 1 : kKC], rv[kDma ? 1 : kKC];
 
     static __device__ __forceinline__ X4 ld(__amdgpu_buffer_rsrc_t rs, int off) {
         if constexpr (sizeof(X4) == 8)
@@ -393,7 +430,7 @@ struct Stage<T, NT, true> {
         return __builtin_amdgcn_make_buffer_rsrc(ub, 0, extent, 0x00020000);
     }
 
-    __device__ __forceinline__ void load(const Params& p, int b, int h, int q0) {
+    __device__ __forceinline__ void load(const Params& p, int b, int h, int q0, T* k_dst, T* v_dst) {
         const int N = p.N;
         const int n0 = threadIdx.x >> 2;
         const int d0 = (threadIdx.x & 3) * 4;
@@ -407,11 +444,34 @@ struct Stage<T, NT, true> {
         rq = ld(qr, (nq * qs2 + d0) * es);
 #pragma unroll
         for (int e = 0; e < 4; ++e) rq[e] = T(static_cast<float>(rq[e]) * p.scale);
+        if constexpr (kDma) {
+            // 16 bytes per lane straight into LDS: lane l of wave w loads half
+            // l&1 of row 32*(4r + w) + l/2; the wave's 64 lanes fill 32
+            // consecutive rows (1 KB) at the wave-uniform LDS address
+            const int lane = threadIdx.x & 63;
+            const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+            const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
+            const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
+            typedef __attribute__((address_space(3))) T LdsT;
+            const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
+            const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
 #pragma unroll
-        for (int k = 0; k < kKC; ++k) {
-            const int n = min(n0 + 64 * k, N - 1);
-            rk[k] = ld(kr, (n * ks2 + d0) * es);
-            rv[k] = ld(vr, (n * vs2 + d0) * es);
+            for (int r = 0; r < kRounds; ++r) {
+                const int row0 = 32 * (4 * r + wave);
+                if (row0 < kRows) {  // wave-uniform
+                    const int n = min(row0 + (lane >> 1), N - 1);
+                    const int half = (lane & 1) * 8;
+                    dma16(kd, kl + row0 * 32, (n * ks2 + half) * es);
+                    dma16(vd, vl + row0 * 32, (n * vs2 + half) * es);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kKC; ++k) {
+                const int n = min(n0 + 64 * k, N - 1);
+                rk[k] = ld(kr, (n * ks2 + d0) * es);
+                rv[k] = ld(vr, (n * vs2 + d0) * es);
+            }
         }
     }
 
@@ -419,14 +479,16 @@ struct Stage<T, NT, true> {
         const int tid = threadIdx.x;
         const int n0 = tid >> 2, d0 = (tid & 3) * 4;
         *reinterpret_cast<X4*>(&q_lds[tid * 4]) = rq;
+        if constexpr (!kDma) {
 #pragma unroll
-        for (int k = 0; k < kKC; ++k) {
-            *reinterpret_cast<X4*>(&k_lds[(tid + k * kThreads) * 4]) = rk[k];
-            if constexpr (v_row_major<T>()) {
-                *reinterpret_cast<X4*>(&vt_lds[(tid + k * kThreads) * 4]) = rv[k];
-            } else {
+            for (int k = 0; k < kKC; ++k) {
+                *reinterpret_cast<X4*>(&k_lds[(tid + k * kThreads) * 4]) = rk[k];
+                if constexpr (v_row_major<T>()) {
+                    *reinterpret_cast<X4*>(&vt_lds[(tid + k * kThreads) * 4]) = rv[k];
+                } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n0 + 64 * k] = rv[k][e];
+                    for (int e = 0; e < 4; ++e) vt_lds[(d0 + e) * kVtStride + n0 + 64 * k] = rv[k][e];
+                }
             }
         }
     }
@@ -500,6 +562,19 @@ __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, 
             bs[t][r] = (16 * t + 4 * g + r) < N ? val : -INFINITY;
         }
     }
+}
+
+
+// max(m[l], m[l ^ 16]) and max(m[l], m[l ^ 32]) with the gfx950 VALU row
+// swaps: with both operands m, v_permlane16_swap returns m[l] and m[l ^ 16]
+// (in some order), v_permlane32_swap m[l] and m[l ^ 32]; no LDS round trip.
+__device__ __forceinline__ float xmax16(float m) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xmax32(float m) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 // One strip (16 queries, NT*16 keys) of one window.
@@ -617,8 +692,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
             }
         }
         float m = fmaxf(m0, m1);
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        m = xmax32(xmax16(m));
         const float mb = m * kLog2e;
         if (c0 > 0) {  // rescale what the earlier chunks accumulated
             const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, kLog2e, -mb));
@@ -719,7 +793,7 @@ swin_attention_d16_kernel(const Params p) {
     constexpr int NP = St::NP;
     __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * 16];
     __shared__ __attribute__((aligned(16))) T k_lds[2][St::kRows * 16];
-    __shared__ __attribute__((aligned(16))) T vt_lds[2][16 * St::kVtStride];
+    __shared__ __attribute__((aligned(16))) T vt_lds[2][St::kVLds];
     __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
 
     uint32_t chunk;
@@ -765,8 +839,14 @@ swin_attention_d16_kernel(const Params p) {
     int code_cur = -1;
     int code_next;
     int b_next = it.window(p, code_next);
-    st.load(p, b_next, h, q0);
+    // tensor mode: the window's boundary flag is read before the next
+    // window's rows are requested, so waiting for it never waits for them
+    bool flag_next = true;
+    if constexpr (kMask != kNoMask && kMask != kMaskRegion)
+        flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
+    st.load(p, b_next, h, q0, k_lds[0], vt_lds[0]);
     st.store(q_lds[0], k_lds[0], vt_lds[0]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
     __syncthreads();
 
     f32x4 bs[NT];
@@ -774,10 +854,13 @@ swin_attention_d16_kernel(const Params p) {
         const int buf = (i - i0) & 1;
         const int b = b_next;
         const int code = code_next;
+        const bool flag = flag_next;
         if (i + 1 < i1) {
             it.next(p);
             b_next = it.window(p, code_next);
-            st.load(p, b_next, h, q0);
+            if constexpr (kMask != kNoMask && kMask != kMaskRegion)
+                flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
+            st.load(p, b_next, h, q0, k_lds[buf ^ 1], vt_lds[buf ^ 1]);
         }
         if (active) {
             if (code != code_cur) {  // workgroup-uniform: new bias (+ mask) tiles
@@ -785,8 +868,7 @@ swin_attention_d16_kernel(const Params p) {
                 code_cur = code;
             }
             bool use_mask = false;
-            if constexpr (kMask != kNoMask && kMask != kMaskRegion)
-                use_mask = p.boundary == nullptr || p.boundary[b] != 0;
+            if constexpr (kMask != kNoMask && kMask != kMaskRegion) use_mask = flag;
             if (use_mask)
                 attend<T, NT, kMask, (kMask != kNoMask && kMask != kMaskRegion), kVec>(
                     p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h, wave, qi, col, g);
@@ -795,6 +877,7 @@ swin_attention_d16_kernel(const Params p) {
                                                   h, wave, qi, col, g);
         }
         if (i + 1 < i1) st.store(q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
         __syncthreads();
     }
 }
