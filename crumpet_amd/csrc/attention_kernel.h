@@ -594,10 +594,18 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
     // Tensor mask through a buffer descriptor spanning exactly the window's
     // [N, N] extent: offsets past it return 0, so no per-key test is needed;
     // padded keys read a finite neighbour (their bias is -inf) and padded
-    // query rows read row N-1 (never stored).  Offsets are immediates.
+    // query rows read row N-1 (never stored).  A lane's 4 keys of a tile are
+    // contiguous in the mask row, so each tile is one 8-byte (16-bit masks)
+    // or 16-byte (fp32 masks) load; the target accesses memory unaligned, so
+    // an odd row stride is fine.  Only the last tile of row N-1 can reach
+    // past the extent, and a range check at dword or access granularity
+    // would then zero in-range keys sharing the load, so those lanes read
+    // that tile again element by element.  Offsets are immediates.
+    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    constexpr int kMaskWords = kMaskBytes;  // 32-bit words per lane and tile
     __amdgpu_buffer_rsrc_t mrsrc;
     int mvoff = 0;
-    uint32_t mq[kUseMask ? 4 * kPrefetch : 1];
+    uint32_t mq[kUseMask ? kMaskWords * kPrefetch : 1];
     if constexpr (kUseMask) {
         const int qr = qi < N ? qi : N - 1;
         // uniform base and extent, kept in scalar registers (see build_tiles)
@@ -610,13 +618,31 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
     }
     auto fetch = [&](int t, int slot) {
         if constexpr (kUseMask) {
+            const int off = mvoff + 16 * t * kMaskBytes;
+            if constexpr (kMaskBytes == 2) {
+                const u32x2v w = __builtin_amdgcn_raw_buffer_load_b64(mrsrc, off, 0, 0);
+                mq[2 * slot] = w[0];
+                mq[2 * slot + 1] = w[1];
+            } else {
+                const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, off, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int off = mvoff + (16 * t + r) * kMaskBytes;
-                if constexpr (kMaskBytes == 2)
-                    mq[4 * slot + r] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off, 0, 0);
-                else
-                    mq[4 * slot + r] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, off, 0, 0);
+                for (int r = 0; r < 4; ++r) mq[4 * slot + r] = w[r];
+            }
+            // the load that reaches past the extent end (row N-1, last tile)
+            // is read again element by element (compile-time tile test)
+            if (t == NT - 1 && qi == N - 1 && 16 * t + 4 * g + 3 >= N) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if constexpr (kMaskBytes == 2) {
+                        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off + 2 * r, 0, 0);
+                        if (r & 1)
+                            mq[2 * slot + (r >> 1)] |= h << 16;
+                        else
+                            mq[2 * slot + (r >> 1)] = h;
+                    } else {
+                        mq[4 * slot + r] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, off + 4 * r, 0, 0);
+                    }
+                }
             }
         }
     };
@@ -653,13 +679,16 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
                 const int slot = t % kPrefetch;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const uint32_t bits = mq[4 * slot + r];
-                    if constexpr (kMask == kMaskF16)
-                        c[r] += static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-                    else if constexpr (kMask == kMaskBF16)
-                        c[r] += __uint_as_float(bits << 16);
-                    else
-                        c[r] += __uint_as_float(bits);
+                    if constexpr (kMask == kMaskF32) {
+                        c[r] += __uint_as_float(mq[4 * slot + r]);
+                    } else {
+                        const uint32_t w = mq[2 * slot + (r >> 1)];
+                        if constexpr (kMask == kMaskF16)
+                            c[r] += static_cast<float>(
+                                __builtin_bit_cast(_Float16, static_cast<uint16_t>(r & 1 ? w >> 16 : w)));
+                        else
+                            c[r] += __uint_as_float(r & 1 ? (w & 0xffff0000u) : (w << 16));
+                    }
                 }
                 if (t + kPrefetch < NT) fetch(t + kPrefetch, slot);
             }

@@ -122,6 +122,27 @@ def test_mask_repeat_by_window_index(oracle, dev):
     _compare(out, ref, dtype, "mask mod nW")
 
 
+@pytest.mark.parametrize("N", [27, 125, 343])
+@pytest.mark.parametrize("mdt", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+def test_random_mask_dtypes_and_odd_row_stride(oracle, dev, mdt, N):
+    """Arbitrary mask values in every position, the mask a column slice of a
+    wider buffer (odd row stride N + 3), N not a multiple of 16: the last key
+    tile of the last query row ends exactly at the end of the mask extent."""
+    dtype = torch.bfloat16 if mdt == torch.bfloat16 else torch.float16
+    B, H, Dh = 6, 2, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 900 + N)
+    bias = _bias(H, N, dtype, 901 + N)
+    g = torch.Generator().manual_seed(902 + N)
+    wide = (torch.randn((3, N, N + 3), generator=g) * 3.0).to(mdt)
+    mask = wide[:, :, :N]  # [3, N, N], row stride N + 3, read as mask[b mod 3]
+    assert mask.stride() == (N * (N + 3), N + 3, 1)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), None, scale=0.25)
+    out = torch.empty_like(q, device=dev)
+    fused_swin_attention_windows(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), wide.to(dev)[:, :, :N], None,
+                                 0.25, out)
+    _compare(out, ref, dtype, f"random {mdt} mask N={N}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_strided_qkv_views_and_strided_out(oracle, dev, dtype):
     """q, k, v as views of a [b, n, 3, H, d] qkv buffer (monai_patch.py:153-154) and
