@@ -184,6 +184,31 @@ __device__ __forceinline__ typename Frag<T>::x4 load_row4(const T* row, int64_t 
     }
 }
 
+// q * scale in fp32, rounded back to the input type (the reference scales q
+// before the dot product: torch-ext/crumpet/fused_attention.py:88).  Applied
+// when Q is written to LDS, not when its load is issued, so no wait for the
+// load lands between the issue of a window's rows and the compute that
+// should hide them.
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::x4 scaled(typename Frag<T>::x4 v, float scale) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = T(static_cast<float>(v[e]) * scale);
+    return v;
+}
+
+// K layout in LDS.  2-byte types: each 16-row key tile stores the first 8
+// dims of its 16 rows (16 B each), then the last 8, so the 32 lanes of a
+// half-wave that read one key fragment (rows 0-15, dims 4g..4g+3, g = 0, 1)
+// cover 256 contiguous bytes; with plain 32-byte rows they would cover only
+// half of each row and collide on the banks.  fp32: plain rows.
+template <typename T>
+__device__ __forceinline__ constexpr int kidx(int row, int d) {
+    if constexpr (sizeof(T) == 2)
+        return (row >> 4) * 256 + (d >> 3) * 128 + (row & 15) * 8 + (d & 7);
+    else
+        return row * 16 + d;
+}
+
 template <typename T>
 __device__ __forceinline__ typename Frag<T>::x4 zero4() {
     typename Frag<T>::x4 r;
@@ -323,11 +348,7 @@ struct Stage {
             r[k] = zero4<T>();
             if (c < kQChunks) {
                 const int n = q0 + (c >> 2);
-                if (n < p.N) {
-                    r[k] = load_row4<T, kVec>(qb + n * p.qs[2], p.qs[3], (c & 3) * 4);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) r[k][e] = T(static_cast<float>(r[k][e]) * p.scale);
-                }
+                if (n < p.N) r[k] = load_row4<T, kVec>(qb + n * p.qs[2], p.qs[3], (c & 3) * 4);
             } else if (c < kChunks) {
                 const int cc = c - kQChunks;
                 const bool isv = cc >= NP * 4;
@@ -340,16 +361,16 @@ struct Stage {
         }
     }
 
-    __device__ __forceinline__ void store(T* q_lds, T* k_lds, T* vt_lds) const {
+    __device__ __forceinline__ void store(float scale, T* q_lds, T* k_lds, T* vt_lds) const {
 #pragma unroll
         for (int k = 0; k < kPerThread; ++k) {
             const int c = threadIdx.x + k * kThreads;
             if (c < kQChunks) {
-                *reinterpret_cast<X4*>(&q_lds[c * 4]) = r[k];
+                *reinterpret_cast<X4*>(&q_lds[c * 4]) = scaled<T>(r[k], scale);
             } else if (c < kChunks) {
                 const int cc = c - kQChunks;
                 if (cc < NP * 4) {
-                    *reinterpret_cast<X4*>(&k_lds[cc * 4]) = r[k];
+                    *reinterpret_cast<X4*>(&k_lds[kidx<T>(cc >> 2, (cc & 3) * 4)]) = r[k];
                 } else {
                     const int c2 = cc - NP * 4;
                     if constexpr (v_row_major<T>()) {
@@ -442,12 +463,12 @@ struct Stage<T, NT, true> {
         constexpr int es = sizeof(T);
         const int nq = min(q0 + n0, N - 1);
         rq = ld(qr, (nq * qs2 + d0) * es);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) rq[e] = T(static_cast<float>(rq[e]) * p.scale);
         if constexpr (kDma) {
-            // 16 bytes per lane straight into LDS: lane l of wave w loads half
-            // l&1 of row 32*(4r + w) + l/2; the wave's 64 lanes fill 32
-            // consecutive rows (1 KB) at the wave-uniform LDS address
+            // 16 bytes per lane straight into LDS: the 64 lanes of wave w in
+            // round r fill the 1 KB of rows 32*(4r + w) .. +31 at a
+            // wave-uniform LDS address, lane l writing its 16-byte chunk l;
+            // which row half each lane fetches sets the layout (kidx for K,
+            // plain rows for V)
             const int lane = threadIdx.x & 63;
             const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
             const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
@@ -459,10 +480,13 @@ struct Stage<T, NT, true> {
             for (int r = 0; r < kRounds; ++r) {
                 const int row0 = 32 * (4 * r + wave);
                 if (row0 < kRows) {  // wave-uniform
-                    const int n = min(row0 + (lane >> 1), N - 1);
-                    const int half = (lane & 1) * 8;
-                    dma16(kd, kl + row0 * 32, (n * ks2 + half) * es);
-                    dma16(vd, vl + row0 * 32, (n * vs2 + half) * es);
+                    // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15)
+                    const int nk = min(row0 + ((lane >> 5) << 4) + (lane & 15), N - 1);
+                    const int hk = ((lane >> 4) & 1) * 8;
+                    dma16(kd, kl + row0 * 32, (nk * ks2 + hk) * es);
+                    // V: plain 32-byte rows (its transpose reads are conflict-free)
+                    const int nv = min(row0 + (lane >> 1), N - 1);
+                    dma16(vd, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
                 }
             }
         } else {
@@ -475,10 +499,10 @@ struct Stage<T, NT, true> {
         }
     }
 
-    __device__ __forceinline__ void store(T* q_lds, T* k_lds, T* vt_lds) const {
+    __device__ __forceinline__ void store(float scale, T* q_lds, T* k_lds, T* vt_lds) const {
         const int tid = threadIdx.x;
         const int n0 = tid >> 2, d0 = (tid & 3) * 4;
-        *reinterpret_cast<X4*>(&q_lds[tid * 4]) = rq;
+        *reinterpret_cast<X4*>(&q_lds[tid * 4]) = scaled<T>(rq, scale);
         if constexpr (!kDma) {
 #pragma unroll
             for (int k = 0; k < kKC; ++k) {
@@ -693,7 +717,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
                 if (t + kPrefetch < NT) fetch(t + kPrefetch, slot);
             }
             if constexpr (sizeof(T) == 2) {
-                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
+                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[kidx<T>(16 * t + col, 4 * g)]);
                 S[u] = Frag<T>::mma16(kf, qf, c);
             } else {
                 const f32x4 kf = *reinterpret_cast<const f32x4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
@@ -874,7 +898,7 @@ swin_attention_d16_kernel(const Params p) {
     if constexpr (kMask != kNoMask && kMask != kMaskRegion)
         flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
     st.load(p, b_next, h, q0, k_lds[0], vt_lds[0]);
-    st.store(q_lds[0], k_lds[0], vt_lds[0]);
+    st.store(p.scale, q_lds[0], k_lds[0], vt_lds[0]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
     __syncthreads();
 
@@ -884,6 +908,14 @@ swin_attention_d16_kernel(const Params p) {
         const int b = b_next;
         const int code = code_next;
         const bool flag = flag_next;
+        // New bias (+ region mask) tiles are built before the next window's
+        // rows are requested: the vector-memory counter retires in order, so
+        // waiting for the bias loads after that request would wait for the
+        // rows as well.
+        if (active && code != code_cur) {  // code is workgroup-uniform
+            build_tiles<NT, kMask>(bs, p, h, qi, g, code, cls_lds);
+            code_cur = code;
+        }
         if (i + 1 < i1) {
             it.next(p);
             b_next = it.window(p, code_next);
@@ -892,10 +924,6 @@ swin_attention_d16_kernel(const Params p) {
             st.load(p, b_next, h, q0, k_lds[buf ^ 1], vt_lds[buf ^ 1]);
         }
         if (active) {
-            if (code != code_cur) {  // workgroup-uniform: new bias (+ mask) tiles
-                build_tiles<NT, kMask>(bs, p, h, qi, g, code, cls_lds);
-                code_cur = code;
-            }
             bool use_mask = false;
             if constexpr (kMask != kNoMask && kMask != kMaskRegion) use_mask = flag;
             if (use_mask)
@@ -905,7 +933,7 @@ swin_attention_d16_kernel(const Params p) {
                 attend<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b,
                                                   h, wave, qi, col, g);
         }
-        if (i + 1 < i1) st.store(q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+        if (i + 1 < i1) st.store(p.scale, q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
         __syncthreads();
     }
