@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--no-eager", action="store_true", help="skip the eager GPU attention chain")
     p.add_argument("--no-blocks", action="store_true", help="skip the config-4 stage block paths")
     p.add_argument("--no-e2e", action="store_true", help="skip the config-5 Swin UNETR forward")
+    p.add_argument("--no-fused-block", action="store_true",
+                   help="skip the fused window-MSA block at the config-5 stage shapes")
     p.add_argument("--profile", action="store_true",
                    help="short fixed launch sequence for rocprofv3 (plus a copy of known size)")
     return p.parse_args()
@@ -269,6 +271,101 @@ def bench_blocks(args, dev):
     return res
 
 
+FUSED_STAGES = [  # config 5 stage shapes at B=4: (name, dim, C, heads, shift)
+    ("s0", 48, 48, 3, 3),
+    ("s1", 24, 96, 6, 3),
+    ("s2", 12, 192, 12, 3),
+    ("s3", 6, 384, 24, 0),
+]
+
+
+def bench_fused_block(args, dev):
+    """The attention half of a Swin block (forward_part1) at the config-5
+    stage shapes, B=4, under fp16 autocast (fp32 block input, fp16 Linear and
+    attention): the fused block kernels (window_qkv_3d -> attention ->
+    window_proj_3d) against the patched unfused path (torch LayerNorm, F.pad,
+    partition kernel, torch Linear, attention kernel, torch Linear,
+    unpartition kernel, crop) and the unpatched eager MONAI chain.  The two
+    projection kernels are also timed alone against their HBM bytes."""
+    import torch
+
+    import crumpet_amd
+    from crumpet_amd import fused_block, monai_patch
+    from crumpet_amd import swin_unetr_compat as sw
+
+    res = {}
+    crumpet_amd.unpatch_monai_swin_unetr()
+    for name, dim, C, H, shift in FUSED_STAGES:
+        B = 4
+        torch.manual_seed(700 + dim)
+        blk = sw.SwinTransformerBlock(dim=C, num_heads=H, window_size=(7, 7, 7),
+                                      shift_size=(shift,) * 3).to(dev).eval()
+        x = seeded((B, dim, dim, dim, C), torch.float32, 710 + dim).to(dev)
+        ws, ss = sw.get_window_size((dim,) * 3, blk.window_size, blk.shift_size)
+        ws, ss = tuple(ws), tuple(ss)
+        padded = tuple(-(-dim // w) * w for w in ws)
+        shifted = any(v > 0 for v in ss)
+        m_eager = sw.compute_mask(padded, ws, ss, dev) if shifted else None
+        m_patch = None
+        if shifted:
+            m_patch = crumpet_amd.compute_attn_mask_3d(*padded, ws, ss, torch.float32, dev)
+            setattr(m_patch, monai_patch._GEOMETRY_ATTR, (*padded, ws, ss))
+
+        def run(fn):
+            def step(i):
+                with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+                    fn()
+            _events_time(step, args.warmup)
+            return _events_time(step, max(10, args.steps // 4))
+
+        t_eager = run(lambda: blk.forward_part1(x, m_eager))
+        assert crumpet_amd.patch_monai_swin_unetr()
+        try:
+            with torch.autocast("cuda", dtype=torch.float16):
+                assert monai_patch._fused_block_supported(blk, x)
+            t_fused = run(lambda: monai_patch._fused_block_forward(blk, x, m_patch, sw))
+            os.environ["CRUMPET_DISABLE_FUSED_BLOCK"] = "1"
+            try:
+                t_unfused = run(lambda: blk.forward_part1(x, m_patch))
+            finally:
+                os.environ.pop("CRUMPET_DISABLE_FUSED_BLOCK", None)
+        finally:
+            crumpet_amd.unpatch_monai_swin_unetr()
+
+        # the two projection kernels alone
+        w_qkv = blk.attn.qkv.weight.detach().half()
+        b_qkv = blk.attn.qkv.bias.detach().half()
+        w_p = blk.attn.proj.weight.detach().half()
+        b_p = blk.attn.proj.bias.detach().half()
+        nw = (padded[0] // ws[0]) * (padded[1] // ws[1]) * (padded[2] // ws[2])
+        n = ws[0] * ws[1] * ws[2]
+        qkv_out = torch.empty((B * nw, n, 3 * C), dtype=torch.float16, device=dev)
+        win = seeded((B * nw, n, C), torch.float16, 720 + dim).to(dev)
+        y = torch.empty((B, dim, dim, dim, C), dtype=torch.float16, device=dev)
+        nrm = blk.norm1
+        t_qkv = _events_time(lambda i: fused_block.window_qkv_3d(
+            x, w_qkv, b_qkv, ws, ss, nrm.weight, nrm.bias, nrm.eps, True, torch.float16, qkv_out), args.steps)
+        t_proj = _events_time(lambda i: fused_block.window_proj_3d(
+            win, w_p, b_p, B, dim, dim, dim, ws, ss, y), args.steps)
+        qkv_bytes = x.numel() * 4 + qkv_out.numel() * 2
+        proj_bytes = win.numel() * 2 + y.numel() * 2
+        gq = qkv_bytes / (t_qkv * 1e-3) / 1e9
+        gp = proj_bytes / (t_proj * 1e-3) / 1e9
+        res[name] = {
+            "shape": [B, dim, dim, dim, C], "heads": H, "window": list(ws), "shift": list(ss),
+            "ms_fused": round(t_fused, 5), "ms_unfused_patched": round(t_unfused, 5),
+            "ms_eager": round(t_eager, 5), "speedup_vs_unfused": round(t_unfused / t_fused, 3),
+            "speedup_vs_eager": round(t_eager / t_fused, 3),
+            "window_qkv": {"ms": round(t_qkv, 5), "bytes": qkv_bytes, "GB_s": round(gq, 1),
+                           "frac_hbm": round(gq / HBM_PEAK_GBS, 4)},
+            "window_proj": {"ms": round(t_proj, 5), "bytes": proj_bytes, "GB_s": round(gp, 1),
+                            "frac_hbm": round(gp / HBM_PEAK_GBS, 4)},
+        }
+        del x, qkv_out, win, y, blk
+        torch.cuda.empty_cache()
+    return res
+
+
 def synthetic_ct(shape, seed):
     """Config 5 input: uniform [0,1] intensities plus smooth Gaussian blobs, clamped to [0,1]."""
     import torch
@@ -442,6 +539,8 @@ def main():
     torch.cuda.empty_cache()
     blocks = {} if args.no_blocks else bench_blocks(args, dev)
     torch.cuda.empty_cache()
+    fused = {} if args.no_fused_block else bench_fused_block(args, dev)
+    torch.cuda.empty_cache()
     e2e = {} if args.no_e2e else bench_e2e(args, dev)
     torch.cuda.empty_cache()
 
@@ -483,6 +582,8 @@ def main():
         components["attention_shifted"] = comp_s
     if blocks:
         components["block_path"] = blocks
+    if fused:
+        components["window_msa_block"] = fused
     if e2e:
         components["swin_unetr_e2e"] = e2e
 

@@ -29,6 +29,8 @@ C_ABI_SYMBOLS = (
     "crumpet_compute_attn_mask_3d",
     "crumpet_fused_swin_attention",
     "crumpet_fused_swin_attention_shifted",
+    "crumpet_window_qkv_3d",
+    "crumpet_window_proj_3d",
 )
 
 OP_NAMES = (
@@ -39,6 +41,8 @@ OP_NAMES = (
     "fused_unshift_unpartition_3d_backward",
     "fused_swin_attention",
     "fused_swin_attention_shifted",
+    "window_qkv_3d",
+    "window_proj_3d",
 )
 
 _hip = None

@@ -4,7 +4,8 @@
 // (torch-ext/torch_binding.cpp:10-31), plus `fused_swin_attention`, which
 // the reference launched from Python through Triton, and
 // `fused_swin_attention_shifted` (attention with the shifted-window mask
-// derived from the volume geometry instead of a mask tensor).  Every impl checks
+// derived from the volume geometry instead of a mask tensor), and the fused
+// block projections `window_qkv_3d` / `window_proj_3d`.  Every impl checks
 // shapes, dtypes and devices (so no launch can index outside its tensors),
 // takes the current HIP stream of the tensor's device (ROCm torch tags HIP
 // devices as "cuda", hence the masquerading guard/stream helpers) and forwards to the
@@ -232,6 +233,96 @@ void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at
         static_cast<float>(scale), stream_of(q)));
 }
 
+// Linear weight [n_out, C] and optional bias [n_out], contiguous, in `dt`.
+void check_linear_params(const at::Tensor& weight, const std::optional<at::Tensor>& bias,
+                         int64_t C, at::ScalarType dt, const at::Device& dev, const char* what) {
+    TORCH_CHECK(weight.dim() == 2 && weight.size(1) == C, what, ": weight must have shape [n_out, ", C,
+                "]");
+    TORCH_CHECK(weight.scalar_type() == dt && weight.device() == dev && weight.is_contiguous(), what,
+                ": weight must be a contiguous tensor of the output dtype on the output's device");
+    if (bias.has_value()) {
+        TORCH_CHECK(bias->dim() == 1 && bias->size(0) == weight.size(0), what,
+                    ": bias must have shape [n_out]");
+        TORCH_CHECK(bias->scalar_type() == dt && bias->device() == dev && bias->is_contiguous(), what,
+                    ": bias must be a contiguous tensor of the output dtype on the output's device");
+    }
+}
+
+void window_qkv_3d(at::Tensor& out, const at::Tensor& x, const std::optional<at::Tensor>& norm_weight,
+                   const std::optional<at::Tensor>& norm_bias, double eps, bool normalize,
+                   const at::Tensor& weight, const std::optional<at::Tensor>& bias, int64_t ws_d,
+                   int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w) {
+    const char* what = "window_qkv_3d";
+    TORCH_CHECK(x.dim() == 5, what, ": x must have shape [B, D, H, W, C]");
+    TORCH_CHECK(x.is_cuda() && out.device() == x.device(), what,
+                ": x and out must be on the same HIP device");
+    TORCH_CHECK(x.is_contiguous() && out.is_contiguous(), what, ": x and out must be contiguous");
+    const int32_t xdt = dtype_code(x.scalar_type());
+    const int32_t dt = dtype_code(out.scalar_type());
+    TORCH_CHECK(xdt >= 0 && dt >= 0, what, ": dtypes must be float32, float16 or bfloat16");
+    const int64_t B = x.size(0), D = x.size(1), H = x.size(2), W = x.size(3), C = x.size(4);
+    check_linear_params(weight, bias, C, out.scalar_type(), x.device(), what);
+    const int64_t n_out = weight.size(0);
+    TORCH_CHECK(ws_d > 0 && ws_h > 0 && ws_w > 0, what, ": window_size values must be positive");
+    const int64_t Dp = (D + ws_d - 1) / ws_d * ws_d, Hp = (H + ws_h - 1) / ws_h * ws_h,
+                  Wp = (W + ws_w - 1) / ws_w * ws_w;
+    const int64_t N = ws_d * ws_h * ws_w;
+    TORCH_CHECK(out.dim() == 3 && out.size(0) == B * (Dp / ws_d) * (Hp / ws_h) * (Wp / ws_w) &&
+                    out.size(1) == N && out.size(2) == n_out,
+                what, ": out must have shape [B*nW, N, n_out] over the volume padded to the window grid");
+    const void* lw = nullptr;
+    const void* lb = nullptr;
+    int32_t ldt = CRUMPET_DTYPE_F32;
+    for (const auto* p : {&norm_weight, &norm_bias}) {
+        if (!p->has_value()) continue;
+        const at::Tensor& t = p->value();
+        TORCH_CHECK(t.dim() == 1 && t.size(0) == C && t.is_contiguous() && t.device() == x.device(), what,
+                    ": LayerNorm parameters must be contiguous [C] tensors on x's device");
+        ldt = dtype_code(t.scalar_type());
+        TORCH_CHECK(ldt >= 0, what, ": LayerNorm parameter dtype must be float32, float16 or bfloat16");
+    }
+    if (norm_weight.has_value() && norm_bias.has_value())
+        TORCH_CHECK(norm_weight->scalar_type() == norm_bias->scalar_type(), what,
+                    ": LayerNorm weight and bias must share a dtype");
+    if (norm_weight.has_value()) lw = norm_weight->data_ptr();
+    if (norm_bias.has_value()) lb = norm_bias->data_ptr();
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
+    check_status(crumpet_window_qkv_3d(out.data_ptr(), dt, x.data_ptr(), xdt, B, D, H, W, C,
+                                       normalize ? 1 : 0, lw, lb, ldt, static_cast<float>(eps),
+                                       weight.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr,
+                                       n_out, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, stream_of(x)));
+}
+
+void window_proj_3d(at::Tensor& out, const at::Tensor& windows, const at::Tensor& weight,
+                    const std::optional<at::Tensor>& bias, int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                    int64_t ss_d, int64_t ss_h, int64_t ss_w) {
+    const char* what = "window_proj_3d";
+    TORCH_CHECK(out.dim() == 5, what, ": out must have shape [B, D, H, W, n_out]");
+    TORCH_CHECK(windows.is_cuda() && out.device() == windows.device(), what,
+                ": windows and out must be on the same HIP device");
+    TORCH_CHECK(windows.is_contiguous() && out.is_contiguous(), what,
+                ": windows and out must be contiguous");
+    TORCH_CHECK(windows.scalar_type() == out.scalar_type(), what, ": windows and out dtypes differ");
+    const int32_t dt = dtype_code(out.scalar_type());
+    TORCH_CHECK(dt >= 0, what, ": dtype must be float32, float16 or bfloat16");
+    TORCH_CHECK(windows.dim() == 3, what, ": windows must have shape [B*nW, N, C]");
+    const int64_t C = windows.size(2);
+    check_linear_params(weight, bias, C, out.scalar_type(), out.device(), what);
+    const int64_t B = out.size(0), D = out.size(1), H = out.size(2), W = out.size(3);
+    TORCH_CHECK(out.size(4) == weight.size(0), what, ": out's last dim must equal n_out");
+    TORCH_CHECK(ws_d > 0 && ws_h > 0 && ws_w > 0, what, ": window_size values must be positive");
+    const int64_t Dp = (D + ws_d - 1) / ws_d * ws_d, Hp = (H + ws_h - 1) / ws_h * ws_h,
+                  Wp = (W + ws_w - 1) / ws_w * ws_w;
+    TORCH_CHECK(windows.size(0) == B * (Dp / ws_d) * (Hp / ws_h) * (Wp / ws_w) &&
+                    windows.size(1) == ws_d * ws_h * ws_w,
+                what, ": windows must have shape [B*nW, N, C] over the volume padded to the window grid");
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
+    check_status(crumpet_window_proj_3d(out.data_ptr(), windows.data_ptr(), dt, B, D, H, W, C,
+                                        weight.data_ptr(), bias.has_value() ? bias->data_ptr() : nullptr,
+                                        weight.size(0), ws_d, ws_h, ws_w, ss_d, ss_h, ss_w,
+                                        stream_of(out)));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(crumpet_ops, ops) {
@@ -264,6 +355,15 @@ TORCH_LIBRARY(crumpet_ops, ops) {
         "int D, int H, int W, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w, "
         "float scale) -> ()",
         kCrumpetOpTags);
+    ops.def(
+        "window_qkv_3d(Tensor! out, Tensor x, Tensor? norm_weight, Tensor? norm_bias, float eps, "
+        "bool normalize, Tensor weight, Tensor? bias, int ws_d, int ws_h, int ws_w, int ss_d, "
+        "int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
+    ops.def(
+        "window_proj_3d(Tensor! out, Tensor windows, Tensor weight, Tensor? bias, int ws_d, int ws_h, "
+        "int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
+        kCrumpetOpTags);
 }
 
 TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
@@ -274,4 +374,6 @@ TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
     ops.impl("fused_unshift_unpartition_3d_backward", &fused_unshift_unpartition_3d_backward);
     ops.impl("fused_swin_attention", &fused_swin_attention);
     ops.impl("fused_swin_attention_shifted", &fused_swin_attention_shifted);
+    ops.impl("window_qkv_3d", &window_qkv_3d);
+    ops.impl("window_proj_3d", &window_proj_3d);
 }

@@ -1,0 +1,472 @@
+// The two token-wise projections of a Swin window-attention block, with the
+// layout changes around them folded into their memory access (gfx950):
+//
+//   window_qkv   : qkv[t] = LN(xpad[src(t)]) @ Wqkv^T + bqkv
+//   window_proj  : y[src(t)] = win[t] @ Wproj^T + bproj   (src(t) inside y)
+//
+// t runs over window-ordered tokens (b, window, position in window) and
+// src(t) is the volume position that the cyclic shift + window partition
+// puts at t: d = (wd*ws_d + ld + ss_d) mod D, likewise for h and w, on the
+// volume zero-padded to the window grid (D, H, W multiples of ws).  Tokens
+// whose src lies in the padding read zeros (the padding is applied after
+// the LayerNorm) and are not stored by window_proj (the crop).
+//
+// This is the eager chain of MONAI's SwinTransformerBlock.forward_part1 and
+// WindowAttention (norm1, F.pad, torch.roll, window_partition, qkv Linear;
+// proj Linear, window_reverse, torch.roll back, crop), as driven by
+// torch-ext/crumpet/monai_patch.py:72-114 and :153-198 in the reference.
+// Fusing it removes the LayerNorm output, the padded copy, the window
+// partition and its inverse as separate HBM round trips: window_qkv reads the
+// block input once and writes qkv once; window_proj reads the attention
+// output once and writes the block output once.
+//
+// Both kernels are one GEMM with M = output features, N = tokens, K = C on
+// the matrix cores: a workgroup of 4 waves owns 64 consecutive window-ordered
+// tokens whose (normalised) rows it stages in LDS as the B operand; each wave
+// walks a quarter of the 16-feature output tiles, reading its weight
+// fragments (the A operand) straight from the L2-resident weight matrix.
+// The MFMA result layout gives each lane 4 consecutive output features of
+// one token, i.e. one 8-byte (fp16/bf16) or 16-byte (fp32) store.
+//
+// Numerics: LayerNorm in fp32 (two passes: mean, then the mean of squared
+// deviations; biased variance, as torch), the normalised value rounded once
+// to the compute type (what autocast does at the Linear's input), products
+// accumulated in fp32, the bias added in fp32, one rounding at the store.
+#include <hip/hip_runtime.h>
+
+#include "crumpet_common.h"
+#include "crumpet_hip.h"
+
+namespace crumpet {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTileTokens = 64;  // tokens per workgroup: 4 MFMA column tiles
+constexpr uint32_t kPadRow = 0xffffffffu;
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// One 16x16x16 multiply-accumulate step D += A B for the compute type.
+template <typename T>
+struct Mma;
+
+template <>
+struct Mma<_Float16> {
+    typedef f16x4 x4;
+    static __device__ __forceinline__ f32x4 step(x4 a, x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mma<__bf16> {
+    typedef bf16x4 x4;
+    static __device__ __forceinline__ f32x4 step(x4 a, x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                         __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mma<float> {
+    typedef f32x4 x4;
+    // four K=4 steps; lane group g contracts k = 4g + j in step j, for A and
+    // B alike, so the 16 products of a row are each taken once
+    static __device__ __forceinline__ f32x4 step(x4 a, x4 b, f32x4 c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+        return c;
+    }
+};
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+    return static_cast<float>(v);
+}
+
+// Element offset of a row padding that keeps 16 consecutive LDS rows on
+// distinct banks for the 8/16-byte fragment reads.
+template <typename T>
+constexpr int row_pad() {
+    return 16 / static_cast<int>(sizeof(T));
+}
+
+struct WinGeom {
+    uint32_t tokens;      // B * nW * vol, window order
+    uint32_t D0, H0, W0;  // the caller's volume
+    uint32_t D, H, W;     // padded to the window grid
+    uint32_t ws_d, ws_h, ws_w;
+    uint32_t ss_d, ss_h, ss_w;
+    FastDiv f_vol, f_nW, f_nWw, f_nWh, f_wsw, f_wsh;
+};
+
+// Row of window-ordered token t in the caller's [B, D0, H0, W0] volume, or
+// kPadRow when the token falls in the padding.
+__device__ __forceinline__ uint32_t token_row(uint32_t t, const WinGeom& g) {
+    uint32_t bw, loc, b, win, tq, ww, wd, wh, lt, lw, ld, lh;
+    g.f_vol.divmod(t, bw, loc);
+    g.f_nW.divmod(bw, b, win);
+    g.f_nWw.divmod(win, tq, ww);
+    g.f_nWh.divmod(tq, wd, wh);
+    g.f_wsw.divmod(loc, lt, lw);
+    g.f_wsh.divmod(lt, ld, lh);
+    uint32_t d = wd * g.ws_d + ld + g.ss_d;
+    uint32_t h = wh * g.ws_h + lh + g.ss_h;
+    uint32_t w = ww * g.ws_w + lw + g.ss_w;
+    d -= (d >= g.D) ? g.D : 0u;
+    h -= (h >= g.H) ? g.H : 0u;
+    w -= (w >= g.W) ? g.W : 0u;
+    if (d >= g.D0 || h >= g.H0 || w >= g.W0) return kPadRow;
+    return ((b * g.D0 + d) * g.H0 + h) * g.W0 + w;
+}
+
+// Four consecutive elements of type T as floats (8- or 16-byte load).
+template <typename T>
+__device__ __forceinline__ f32x4 load4(const T* p) {
+    f32x4 r;
+    if constexpr (sizeof(T) == 4) {
+        r = *reinterpret_cast<const f32x4*>(p);
+    } else {
+        typedef T T4 __attribute__((ext_vector_type(4)));
+        const T4 v = *reinterpret_cast<const T4*>(p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = to_f32(v[e]);
+    }
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ void store4(T* p, f32x4 v) {
+    typedef T T4 __attribute__((ext_vector_type(4)));
+    T4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = static_cast<T>(v[e]);
+    *reinterpret_cast<T4*>(p) = o;
+}
+
+// Per-channel LayerNorm parameter (fp32 or the input's type), 4 at a time.
+__device__ __forceinline__ f32x4 load_param4(const void* p, int32_t dtype, int c, float dflt) {
+    if (p == nullptr) return f32x4{dflt, dflt, dflt, dflt};
+    if (dtype == CRUMPET_DTYPE_F32) return load4(static_cast<const float*>(p) + c);
+    if (dtype == CRUMPET_DTYPE_F16) return load4(static_cast<const _Float16*>(p) + c);
+    return load4(static_cast<const __bf16*>(p) + c);
+}
+
+// GEMM over the staged tile: out^T[f][t] = sum_k W[f][k] a[t][k] (+ bias[f]).
+// Wave w takes feature tiles w, w+4, ...; lane (col = l % 16, g = l / 16)
+// ends with features 16 ft + 4g .. +3 of token 16 s + col for s = 0..3 and
+// hands them to `store(token_in_tile, feature, values)`.
+template <typename Tc, typename Store>
+__device__ __forceinline__ void tile_gemm(const Tc* __restrict__ a_lds, int stride, const Tc* __restrict__ w,
+                                          const Tc* __restrict__ bias, int C, int n_out, Store store) {
+    typedef typename Mma<Tc>::x4 X4;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int ksteps = C >> 4;
+    for (int ft = wave; ft < (n_out >> 4); ft += 4) {
+        const Tc* wrow = w + int64_t(16 * ft + col) * C + 4 * g;
+        f32x4 acc[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int kk = 0; kk < ksteps; ++kk) {
+            const X4 wf = *reinterpret_cast<const X4*>(wrow + 16 * kk);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const X4 bf = *reinterpret_cast<const X4*>(&a_lds[(16 * s + col) * stride + 16 * kk + 4 * g]);
+                acc[s] = Mma<Tc>::step(wf, bf, acc[s]);
+            }
+        }
+        const int f0 = 16 * ft + 4 * g;
+        const f32x4 b4 = bias ? load4(bias + f0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) store(16 * s + col, f0, acc[s] + b4);
+    }
+}
+
+// LN + pad + shift + partition + qkv projection.  kCpl: 4-element chunks of
+// a token row held per lane (4 lanes per token), C <= 16 * kCpl.
+template <typename Tx, typename Tc, int kCpl>
+__global__ void __launch_bounds__(kThreads)
+window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln_w, const void* ln_b,
+                  int32_t ln_dtype, int32_t normalize, float eps, const Tc* __restrict__ w,
+                  const Tc* __restrict__ bias, int32_t C, int32_t n_out, const WinGeom g) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    Tc* a_lds = reinterpret_cast<Tc*>(smem);
+    const int stride = C + row_pad<Tc>();
+    const uint32_t t0 = blockIdx.x * kTileTokens;
+    {
+        // 16 tokens per wave, 4 lanes per token; lane part p holds the
+        // chunks p, p + 4, ... (channels 4c .. 4c + 3 of chunk c)
+        const int lane = threadIdx.x & 63;
+        const int tl = (threadIdx.x >> 6) * 16 + (lane >> 2);
+        const int part = lane & 3;
+        const int nch = C >> 2;
+        const uint32_t t = t0 + tl;
+        const uint32_t row = t < g.tokens ? token_row(t, g) : kPadRow;
+        f32x4 v[kCpl];
+        const Tx* xr = x + int64_t(row == kPadRow ? 0 : row) * C;
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j) {
+            const int c = part + 4 * j;
+            v[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (c < nch && row != kPadRow) v[j] = load4(xr + 4 * c);
+        }
+        if (normalize && row != kPadRow) {
+            float s = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) s += (v[j][0] + v[j][1]) + (v[j][2] + v[j][3]);
+            s += __shfl_xor(s, 1, 4);
+            s += __shfl_xor(s, 2, 4);
+            const float mean = s / static_cast<float>(C);
+            float q = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                if (part + 4 * j < nch) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float dv = v[j][e] - mean;
+                        q = __builtin_fmaf(dv, dv, q);
+                    }
+                }
+            }
+            q += __shfl_xor(q, 1, 4);
+            q += __shfl_xor(q, 2, 4);
+            const float rstd = rsqrtf(q / static_cast<float>(C) + eps);
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const int c = part + 4 * j;
+                if (c < nch) {
+                    const f32x4 gm = load_param4(ln_w, ln_dtype, 4 * c, 1.0f);
+                    const f32x4 bt = load_param4(ln_b, ln_dtype, 4 * c, 0.0f);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[j][e] = __builtin_fmaf((v[j][e] - mean) * rstd, gm[e], bt[e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kCpl; ++j) {
+            const int c = part + 4 * j;
+            if (c < nch) store4(&a_lds[tl * stride + 4 * c], v[j]);
+        }
+    }
+    __syncthreads();
+    tile_gemm<Tc>(a_lds, stride, w, bias, C, n_out, [&](int tl, int f0, f32x4 r) {
+        const uint32_t t = t0 + tl;
+        if (t < g.tokens) store4(out + int64_t(t) * n_out + f0, r);
+    });
+}
+
+// proj projection + inverse partition + reverse shift + crop.
+template <typename Tc>
+__global__ void __launch_bounds__(kThreads)
+window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __restrict__ w,
+                   const Tc* __restrict__ bias, int32_t C, int32_t n_out, const WinGeom g) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+    Tc* a_lds = reinterpret_cast<Tc*>(smem);
+    const int stride = C + row_pad<Tc>();
+    const uint32_t t0 = blockIdx.x * kTileTokens;
+    // the tile's 64 window-ordered rows are contiguous: 4-element chunks
+    const int nch = C >> 2;
+    const uint32_t rows = min(uint32_t(kTileTokens), g.tokens - t0);
+    const Tc* src = win + int64_t(t0) * C;
+    for (int i = threadIdx.x; i < kTileTokens * nch; i += kThreads) {
+        const int r = i / nch;
+        const int c = i - r * nch;
+        f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        if (uint32_t(r) < rows) v = load4(src + int64_t(r) * C + 4 * c);
+        store4(&a_lds[r * stride + 4 * c], v);
+    }
+    __syncthreads();
+    tile_gemm<Tc>(a_lds, stride, w, bias, C, n_out, [&](int tl, int f0, f32x4 r) {
+        const uint32_t t = t0 + tl;
+        if (t >= g.tokens) return;
+        const uint32_t row = token_row(t, g);
+        if (row != kPadRow) store4(y + int64_t(row) * n_out + f0, r);
+    });
+}
+
+int elem_size(int32_t dtype) {
+    switch (dtype) {
+        case CRUMPET_DTYPE_F32: return 4;
+        case CRUMPET_DTYPE_F16: return 2;
+        case CRUMPET_DTYPE_BF16: return 2;
+        default: return 0;
+    }
+}
+
+// Shared validation; fills g.  The caller's volume is [B, D, H, W] with
+// channels C_in; tokens run over the volume padded to the window grid.
+int make_geometry(const char* what, int64_t B, int64_t D, int64_t H, int64_t W, int64_t ws_d,
+                  int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w, WinGeom& g) {
+    if (B < 0 || D <= 0 || H <= 0 || W <= 0)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: B must be non-negative and D, H, W positive", what);
+    if (ws_d <= 0 || ws_h <= 0 || ws_w <= 0)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: window_size values must be positive", what);
+    if (ss_d < 0 || ss_d >= ws_d || ss_h < 0 || ss_h >= ws_h || ss_w < 0 || ss_w >= ws_w)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                    "%s: shift_size must satisfy 0 <= shift < window_size", what);
+    const int64_t Dp = (D + ws_d - 1) / ws_d * ws_d;
+    const int64_t Hp = (H + ws_h - 1) / ws_h * ws_h;
+    const int64_t Wp = (W + ws_w - 1) / ws_w * ws_w;
+    const int64_t tokens = B * Dp * Hp * Wp;
+    if (tokens >= (int64_t(1) << 31) - kTileTokens || B * D * H * W >= (int64_t(1) << 31))
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: more than 2^31 tokens", what);
+    g.tokens = static_cast<uint32_t>(tokens);
+    g.D0 = D; g.H0 = H; g.W0 = W;
+    g.D = Dp; g.H = Hp; g.W = Wp;
+    g.ws_d = ws_d; g.ws_h = ws_h; g.ws_w = ws_w;
+    g.ss_d = ss_d; g.ss_h = ss_h; g.ss_w = ss_w;
+    const uint32_t nWh = Hp / ws_h, nWw = Wp / ws_w;
+    g.f_vol.init(ws_d * ws_h * ws_w);
+    g.f_nW.init((Dp / ws_d) * nWh * nWw);
+    g.f_nWw.init(nWw);
+    g.f_nWh.init(nWh);
+    g.f_wsw.init(ws_w);
+    g.f_wsh.init(ws_h);
+    return CRUMPET_OK;
+}
+
+int check_linear(const char* what, int64_t C, int64_t n_out, int32_t dtype, const void* weight) {
+    if (C <= 0 || C % 16 != 0)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: channels (%lld) must be a positive multiple of 16",
+                    what, (long long)C);
+    if (n_out <= 0 || n_out % 16 != 0)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: output features (%lld) must be a positive multiple of 16",
+                    what, (long long)n_out);
+    if (elem_size(dtype) == 0)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported compute dtype %d", what, dtype);
+    if (weight == nullptr) return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: null weight", what);
+    const int64_t lds = int64_t(kTileTokens) * (C + 16 / elem_size(dtype)) * elem_size(dtype);
+    if (lds > kMaxLdsBytes)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: %lld channels of %d bytes exceed the staging tile",
+                    what, (long long)C, elem_size(dtype));
+    return CRUMPET_OK;
+}
+
+template <typename Tx, typename Tc>
+void launch_qkv(int cpl, dim3 grid, size_t lds, hipStream_t s, void* out, const void* x,
+                const void* ln_w, const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps,
+                const void* w, const void* bias, int32_t C, int32_t n_out, const WinGeom& g) {
+#define CRUMPET_QKV(K)                                                                            \
+    hipLaunchKernelGGL((window_qkv_kernel<Tx, Tc, K>), grid, dim3(kThreads), lds, s,             \
+                       static_cast<Tc*>(out), static_cast<const Tx*>(x), ln_w, ln_b, ln_dtype,  \
+                       normalize, eps, static_cast<const Tc*>(w), static_cast<const Tc*>(bias), \
+                       C, n_out, g)
+    if (cpl <= 3)
+        CRUMPET_QKV(3);
+    else if (cpl <= 6)
+        CRUMPET_QKV(6);
+    else if (cpl <= 12)
+        CRUMPET_QKV(12);
+    else
+        CRUMPET_QKV(24);
+#undef CRUMPET_QKV
+}
+
+template <typename Tx>
+void launch_qkv_x(int32_t dtype, int cpl, dim3 grid, size_t lds, hipStream_t s, void* out,
+                  const void* x, const void* ln_w, const void* ln_b, int32_t ln_dtype, int32_t normalize,
+                  float eps, const void* w, const void* bias, int32_t C, int32_t n_out, const WinGeom& g) {
+    if (dtype == CRUMPET_DTYPE_F16)
+        launch_qkv<Tx, _Float16>(cpl, grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias,
+                                 C, n_out, g);
+    else if (dtype == CRUMPET_DTYPE_BF16)
+        launch_qkv<Tx, __bf16>(cpl, grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias,
+                               C, n_out, g);
+    else
+        launch_qkv<Tx, float>(cpl, grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias,
+                              C, n_out, g);
+}
+
+}  // namespace
+}  // namespace crumpet
+
+using namespace crumpet;
+
+extern "C" int crumpet_window_qkv_3d(void* out, int32_t dtype, const void* x, int32_t x_dtype,
+                                     int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                     int32_t normalize, const void* ln_weight, const void* ln_bias,
+                                     int32_t ln_dtype, float eps, const void* weight, const void* bias,
+                                     int64_t n_out, int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                     int64_t ss_d, int64_t ss_h, int64_t ss_w, void* stream) {
+    const char* what = "crumpet_window_qkv_3d";
+    WinGeom g;
+    int st = make_geometry(what, B, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, g);
+    if (st != CRUMPET_OK) return st;
+    st = check_linear(what, C, n_out, dtype, weight);
+    if (st != CRUMPET_OK) return st;
+    if (elem_size(x_dtype) == 0)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported input dtype %d", what, x_dtype);
+    if (C > 16 * 24)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: at most 384 channels", what);
+    if (normalize && (ln_weight || ln_bias) && ln_dtype != CRUMPET_DTYPE_F32 && ln_dtype != x_dtype)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                    "%s: LayerNorm parameters must be float32 or the input dtype", what);
+    if (!(eps >= 0.0f))
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: eps must be non-negative", what);
+    if (g.tokens == 0) return CRUMPET_OK;
+    if (out == nullptr || x == nullptr)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: null data pointer", what);
+    if ((reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(x) |
+         reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+         reinterpret_cast<uintptr_t>(ln_weight) | reinterpret_cast<uintptr_t>(ln_bias)) % 16 != 0)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: pointers must be 16-byte aligned", what);
+    const int es = elem_size(dtype);
+    const size_t lds = size_t(kTileTokens) * (C + 16 / es) * es;
+    const dim3 grid((g.tokens + kTileTokens - 1) / kTileTokens);
+    const int cpl = static_cast<int>(C / 16);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int32_t ci = static_cast<int32_t>(C), no = static_cast<int32_t>(n_out);
+    if (x_dtype == CRUMPET_DTYPE_F32)
+        launch_qkv_x<float>(dtype, cpl, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                            weight, bias, ci, no, g);
+    else if (x_dtype == CRUMPET_DTYPE_F16)
+        launch_qkv_x<_Float16>(dtype, cpl, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize,
+                               eps, weight, bias, ci, no, g);
+    else
+        launch_qkv_x<__bf16>(dtype, cpl, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize,
+                             eps, weight, bias, ci, no, g);
+    return check_launch(what);
+}
+
+extern "C" int crumpet_window_proj_3d(void* y, const void* windows, int32_t dtype, int64_t B, int64_t D,
+                                      int64_t H, int64_t W, int64_t C, const void* weight,
+                                      const void* bias, int64_t n_out, int64_t ws_d, int64_t ws_h,
+                                      int64_t ws_w, int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                      void* stream) {
+    const char* what = "crumpet_window_proj_3d";
+    WinGeom g;
+    int st = make_geometry(what, B, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, g);
+    if (st != CRUMPET_OK) return st;
+    st = check_linear(what, C, n_out, dtype, weight);
+    if (st != CRUMPET_OK) return st;
+    if (g.tokens == 0) return CRUMPET_OK;
+    if (y == nullptr || windows == nullptr)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: null data pointer", what);
+    if ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(windows) |
+         reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias)) % 16 != 0)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: pointers must be 16-byte aligned", what);
+    const int es = elem_size(dtype);
+    const size_t lds = size_t(kTileTokens) * (C + 16 / es) * es;
+    const dim3 grid((g.tokens + kTileTokens - 1) / kTileTokens);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int32_t ci = static_cast<int32_t>(C), no = static_cast<int32_t>(n_out);
+#define CRUMPET_PROJ(T)                                                                           \
+    hipLaunchKernelGGL((window_proj_kernel<T>), grid, dim3(kThreads), lds, s, static_cast<T*>(y), \
+                       static_cast<const T*>(windows), static_cast<const T*>(weight),            \
+                       static_cast<const T*>(bias), ci, no, g)
+    if (dtype == CRUMPET_DTYPE_F16)
+        CRUMPET_PROJ(_Float16);
+    else if (dtype == CRUMPET_DTYPE_BF16)
+        CRUMPET_PROJ(__bf16);
+    else
+        CRUMPET_PROJ(float);
+#undef CRUMPET_PROJ
+    return check_launch(what);
+}

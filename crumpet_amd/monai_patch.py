@@ -7,7 +7,11 @@ the originals; True / False likewise) replace
 
 * ``SwinTransformerBlock.forward_part1``: norm1, pad to the window grid,
   ``fused_shift_partition_3d``, window attention,
-  ``fused_unshift_unpartition_3d``, crop (reference :72-114);
+  ``fused_unshift_unpartition_3d``, crop (reference :72-114).  In inference
+  mode, with a LayerNorm norm1 and Linear qkv / proj, the whole method runs
+  as three kernels instead (``crumpet_amd.fused_block``): norm1 + pad +
+  shift + partition + qkv in one, the fused attention, and proj + reverse +
+  unshift + crop in one (opt out with ``CRUMPET_DISABLE_FUSED_BLOCK=1``);
 * ``BasicLayer.forward``: channels-last stage loop with the cached
   ``compute_attn_mask_3d`` mask (reference :201-232);
 * ``WindowAttention.forward``: the eager ``q k^T + bias + mask -> softmax
@@ -49,6 +53,7 @@ import torch.nn.functional as F
 
 from . import compute_attn_mask_3d, fused_shift_partition_3d, fused_unshift_unpartition_3d
 from .fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
+from .fused_block import fused_window_msa_3d
 
 _STATE: dict[str, Any] = {}
 _REQUIRED = ("SwinTransformerBlock", "BasicLayer", "WindowAttention", "get_window_size")
@@ -85,11 +90,67 @@ def _as_triple(value) -> tuple[int, int, int]:
     return tuple(int(v) for v in value)
 
 
+def _fused_block_enabled() -> bool:
+    """Opt-out of the fused block projections via ``CRUMPET_DISABLE_FUSED_BLOCK=1``."""
+    return os.environ.get("CRUMPET_DISABLE_FUSED_BLOCK", "0") != "1"
+
+
+def _compute_dtype(x: torch.Tensor) -> torch.dtype:
+    """The dtype the block's Linear layers run in: autocast's, else x's."""
+    if torch.is_autocast_enabled(x.device.type):
+        return torch.get_autocast_dtype(x.device.type)
+    return x.dtype
+
+
+def _fused_block_supported(block, x: torch.Tensor) -> bool:
+    """Inference-mode blocks whose attention half the fused block kernels
+    cover: LayerNorm norm1 over C, Linear qkv / proj, head dimension 16, no
+    attention dropout, C a multiple of 16 that fits the staging tile."""
+    attn = block.attn
+    c = x.shape[-1]
+    if block.training or not (_fused_attn_enabled() and _fused_block_enabled()):
+        return False
+    if x.device.type != "cuda" or x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        return False
+    norm = block.norm1
+    if not isinstance(norm, torch.nn.LayerNorm) or tuple(norm.normalized_shape) != (c,):
+        return False
+    if not isinstance(attn.qkv, torch.nn.Linear) or not isinstance(attn.proj, torch.nn.Linear):
+        return False
+    if attn.qkv.out_features != 3 * c or attn.proj.in_features != c or attn.proj.out_features != c:
+        return False
+    if attn.attn_drop.p != 0.0 or attn.num_heads * 16 != c:
+        return False
+    esize = torch.empty((), dtype=_compute_dtype(x)).element_size()
+    return c % 16 == 0 and c <= 384 and 64 * (c + 16 // esize) * esize <= 64 * 1024
+
+
+def _fused_block_forward(block, x, mask_matrix, swin):
+    """forward_part1 as three kernels: window_qkv_3d (norm1, pad, shift,
+    partition, qkv), the fused attention, window_proj_3d (proj, reverse,
+    unshift, crop)."""
+    b, d, h, w, c = x.shape
+    window_size, shift_size = swin.get_window_size((d, h, w), block.window_size, block.shift_size)
+    ws = _as_triple(window_size)
+    ss = _as_triple(shift_size)
+    padded = tuple(-(-n // k) * k for n, k in zip((d, h, w), ws))
+    attn = block.attn
+    n = ws[0] * ws[1] * ws[2]
+    idx = attn.relative_position_index[:n, :n].reshape(-1)
+    bias = attn.relative_position_bias_table.t()[:, idx].view(attn.num_heads, n, n)
+    shifted = any(s > 0 for s in ss)
+    region = shifted and getattr(mask_matrix, _GEOMETRY_ATTR, None) == (*padded, ws, ss)
+    return fused_window_msa_3d(x, block.norm1, attn.qkv, attn.proj, bias, attn.num_heads, attn.scale, ws, ss,
+                               mask=mask_matrix if shifted else None, region=region, dtype=_compute_dtype(x))
+
+
 def _patched_forward_part1(original, swin):
     @functools.wraps(original)
     def forward_part1(self, x, mask_matrix):
         if x.dim() != 5:
             return original(self, x, mask_matrix)
+        if _fused_block_supported(self, x):
+            return _fused_block_forward(self, x, mask_matrix, swin)
         x = self.norm1(x)
         b, d, h, w, c = x.shape
         window_size, shift_size = swin.get_window_size((d, h, w), self.window_size, self.shift_size)

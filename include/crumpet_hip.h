@@ -225,6 +225,64 @@ CRUMPET_API int crumpet_fused_swin_attention_shifted(
     float scale,
     void* stream);
 
+/*
+ * Window-ordered qkv projection of a Swin window-attention block, with the
+ * layout work before it fused into its operand gather:
+ *
+ *   out[t, :] = LN(xpad[src(t)]) @ weight^T + bias        out: [B*nW, N, n_out]
+ *
+ * x is the block input [B, D, H, W, C] (channels-last, contiguous, x_dtype).
+ * xpad is x zero-padded at the end of each axis to multiples of the window
+ * (padding applied after the LayerNorm, so padded tokens project to `bias`).
+ * Token t = (b*nW + win)*N + loc runs in window order, and src(t) is the
+ * position the cyclic shift by -ss and the window partition place at t
+ * (the same order as crumpet_shift_partition_3d on xpad).
+ *
+ * normalize != 0 applies LayerNorm over C in fp32 (biased variance, eps);
+ * ln_weight / ln_bias are optional (NULL = 1 / 0), fp32 or x_dtype
+ * (ln_dtype).  weight [n_out, C] row-major and bias [n_out] (or NULL) are
+ * in `dtype`, the compute and output type; the normalised input is rounded
+ * to it once, products accumulate in fp32.  C and n_out are multiples of 16,
+ * C <= 384 and 64*(C + 16/esize)*esize <= 64 KiB; every pointer 16-byte
+ * aligned.
+ *
+ * No counterpart in the reference: it fuses the norm1 / F.pad / roll /
+ * window_partition / qkv-Linear chain that torch-ext/crumpet/monai_patch.py
+ * :79-97 and :153 run before the fused attention.
+ */
+CRUMPET_API int crumpet_window_qkv_3d(void* out, int32_t dtype,
+                                      const void* x, int32_t x_dtype,
+                                      int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                      int32_t normalize, const void* ln_weight,
+                                      const void* ln_bias, int32_t ln_dtype, float eps,
+                                      const void* weight, const void* bias, int64_t n_out,
+                                      int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                      int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                      void* stream);
+
+/*
+ * Output projection of a Swin window-attention block, with the inverse
+ * partition, reverse shift and crop fused into its store:
+ *
+ *   y[src(t), :] = windows[t, :] @ weight^T + bias       for src(t) inside y
+ *
+ * windows [B*nW, N, C] (window order over the volume padded to the window
+ * grid, as crumpet_window_qkv_3d), y [B, D, H, W, n_out] (the caller's
+ * unpadded volume; tokens in the padding are dropped).  windows, weight
+ * [n_out, C], bias [n_out] (or NULL) and y share `dtype`; fp32 accumulation.
+ * Same size and alignment rules as crumpet_window_qkv_3d.
+ *
+ * No counterpart in the reference: it fuses the proj-Linear / window_reverse
+ * / roll / crop chain of torch-ext/crumpet/monai_patch.py:196-197 and
+ * :98-111.
+ */
+CRUMPET_API int crumpet_window_proj_3d(void* y, const void* windows, int32_t dtype,
+                                       int64_t B, int64_t D, int64_t H, int64_t W, int64_t C,
+                                       const void* weight, const void* bias, int64_t n_out,
+                                       int64_t ws_d, int64_t ws_h, int64_t ws_w,
+                                       int64_t ss_d, int64_t ss_h, int64_t ss_w,
+                                       void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -328,3 +328,86 @@ def attention(q, k, v, bias, mask=None, boundary=None, scale=None, dtype=np.floa
         p /= p.sum(axis=-1, keepdims=True)
         out[b0:b1] = np.matmul(p, v[b0:b1])
     return out
+
+
+# --------------------------------------------------------------------------
+# fused window-MSA block projections (the chain around the attention)
+# --------------------------------------------------------------------------
+
+def round_to(a, dtype: str) -> np.ndarray:
+    """Round to float16 / bfloat16 / float32 (nearest even) and return float64.
+
+    The 16-bit types are reached through float32, as in the kernels and the
+    autocast chain, whose values are float32 before the cast.  bfloat16 (no
+    numpy type) keeps the upper 16 bits of the float32 value after adding
+    0x7FFF plus the lowest kept bit (round half to even).
+    """
+    a = np.asarray(a, dtype=np.float64)
+    if dtype == "float64":
+        return a
+    if dtype == "float32":
+        return a.astype(np.float32).astype(np.float64)
+    if dtype == "float16":
+        return a.astype(np.float32).astype(np.float16).astype(np.float64)
+    if dtype == "bfloat16":
+        u = a.astype(np.float32).view(np.uint32).astype(np.uint64)
+        u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+        return u.astype(np.uint32).view(np.float32).astype(np.float64)
+    raise ValueError(dtype)
+
+
+def _padded_dims(D, H, W, ws):
+    ws = _triple(ws)
+    return tuple(-(-d // w) * w for d, w in zip((D, H, W), ws))
+
+
+def layer_norm(x, weight=None, bias=None, eps: float = 1e-5) -> np.ndarray:
+    """torch.nn.LayerNorm over the last axis in float64: biased variance, eps
+    inside the square root, optional affine weight / bias."""
+    x = np.asarray(x, dtype=np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = np.square(x - mean).mean(axis=-1, keepdims=True)
+    y = (x - mean) / np.sqrt(var + eps)
+    if weight is not None:
+        y = y * np.asarray(weight, dtype=np.float64)
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float64)
+    return y
+
+
+def window_qkv(x, ws, ss, weight, bias=None, norm_weight=None, norm_bias=None, eps: float = 1e-5,
+               normalize: bool = True, dtype: str = "float16") -> np.ndarray:
+    """[B*nW, N, n_out]: the eager chain of monai_patch.py:79-97 plus the qkv
+    Linear of :153 -- norm1, zero padding at the end of each axis to the
+    window grid (after the norm), roll by -ss, window partition, Linear.
+
+    float64 arithmetic, with the two roundings of the autocast chain: the
+    LayerNorm output (the Linear's input) and the Linear's output are rounded
+    to ``dtype``.  ``weight`` / ``bias`` are taken as given (pass values
+    already rounded to ``dtype``).
+    """
+    x = np.asarray(x, dtype=np.float64)
+    B, D, H, W, C = x.shape
+    a = layer_norm(x, norm_weight, norm_bias, eps) if normalize else x
+    a = round_to(a, dtype)
+    Dp, Hp, Wp = _padded_dims(D, H, W, ws)
+    ap = np.zeros((B, Dp, Hp, Wp, C), dtype=np.float64)
+    ap[:, :D, :H, :W] = a
+    win = np_shift_partition(ap, ws, ss)
+    y = win @ np.asarray(weight, dtype=np.float64).T
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float64)
+    return round_to(y, dtype)
+
+
+def window_proj(windows, B, D, H, W, ws, ss, weight, bias=None, dtype: str = "float16") -> np.ndarray:
+    """[B, D, H, W, n_out]: the proj Linear of monai_patch.py:196-197, then the
+    window reverse on the padded grid, roll by +ss and the crop of :98-111.
+    float64 arithmetic, output rounded to ``dtype``."""
+    y = np.asarray(windows, dtype=np.float64) @ np.asarray(weight, dtype=np.float64).T
+    if bias is not None:
+        y = y + np.asarray(bias, dtype=np.float64)
+    y = round_to(y, dtype)
+    Dp, Hp, Wp = _padded_dims(D, H, W, ws)
+    vol = np_unshift_unpartition(y, B, Dp, Hp, Wp, y.shape[-1], ws, ss)
+    return np.ascontiguousarray(vol[:, :D, :H, :W])

@@ -1,0 +1,171 @@
+"""GPU parity of the fused window-MSA block projections (window_qkv_3d,
+window_proj_3d) with the oracle, and of the whole fused forward_part1 with
+the eager MONAI-style block.
+
+Kernel vs oracle (oracle.window_qkv / window_proj, float64 with the
+autocast roundings): within 4 ulps of the compute dtype relative to
+max(|ref|, 1) -- the LayerNorm output may round to the neighbouring value
+near a rounding boundary (fp32 vs float64 statistics), and fp32
+accumulation differs from float64 by far less than one output ulp.
+Shapes: the Swin UNETR stages at window 7 (padded 12^3, shifted 14^3, the
+7^3 / 6^3 deep stages) and a non-cubic padded case.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from crumpet_amd import fused_block, monai_patch
+from crumpet_amd import swin_unetr_compat as sw
+from helpers import seeded
+
+pytestmark = pytest.mark.gpu
+
+CASES = [  # name, (B, D, H, W, C), ws, ss
+    ("s0pad", (2, 12, 12, 12, 48), (7, 7, 7), (3, 3, 3)),
+    ("s1", (1, 14, 14, 14, 96), (7, 7, 7), (3, 3, 3)),
+    ("s2", (1, 7, 7, 7, 192), (7, 7, 7), (0, 0, 0)),
+    ("s3monai", (2, 6, 6, 6, 384), (6, 6, 6), (0, 0, 0)),
+    ("noncubic", (1, 7, 9, 5, 32), (7, 3, 5), (2, 1, 0)),
+]
+DTYPES = [  # (x dtype, compute dtype)
+    (torch.float32, torch.float16),
+    (torch.float32, torch.bfloat16),
+    (torch.float32, torch.float32),
+    (torch.float16, torch.float16),
+    (torch.bfloat16, torch.bfloat16),
+]
+ULP = {torch.float16: 2 ** -10, torch.bfloat16: 2 ** -7, torch.float32: 2 ** -18}
+NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16", torch.float32: "float32"}
+
+
+def _compare(got: torch.Tensor, want: np.ndarray, dtype, what: str):
+    g = got.float().cpu().double().numpy()
+    assert np.isfinite(g).all()
+    err = np.abs(g - want)
+    bound = 4 * ULP[dtype] * np.maximum(np.abs(want), 1.0)
+    worst = float((err / bound).max())
+    print(f"{what}: max-abs {err.max():.3e}, worst err/bound {worst:.2f}", flush=True)
+    assert worst <= 1.0, f"{what}: error {err.max()} beyond 4 ulps"
+
+
+def _skip_unsupported(C, cdt):
+    es = torch.empty((), dtype=cdt).element_size()
+    if 64 * (C + 16 // es) * es > 64 * 1024:
+        pytest.skip(f"C={C} in {cdt} exceeds the staging tile (unfused path)")
+
+
+@pytest.mark.parametrize("dts", DTYPES, ids=lambda d: f"{NAME[d[0]]}-{NAME[d[1]]}")
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_window_qkv_matches_oracle(oracle, dev, case, dts):
+    name, shape, ws, ss = case
+    xdt, cdt = dts
+    C = shape[-1]
+    _skip_unsupported(C, cdt)
+    print(f"window_qkv {name} {xdt}->{cdt}", flush=True)
+    x = (seeded(shape, torch.float32, 40) * 2.0 + 0.5).to(xdt)
+    gw = seeded((C,), torch.float32, 41) * 0.5 + 1.0
+    gb = seeded((C,), torch.float32, 42) * 0.1
+    w = (seeded((3 * C, C), torch.float32, 43) / C ** 0.5).to(cdt)
+    b = (seeded((3 * C,), torch.float32, 44) * 0.1).to(cdt)
+    got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), b.to(dev), ws, ss, gw.to(dev), gb.to(dev), 1e-5, True,
+                                    cdt)
+    want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), b.double().numpy(),
+                             gw.double().numpy(), gb.double().numpy(), 1e-5, True, NAME[cdt])
+    assert got.shape == want.shape
+    _compare(got, want, cdt, f"window_qkv {name}")
+
+
+def test_window_qkv_options(oracle, dev):
+    """No LayerNorm, no bias, LayerNorm parameters in the input's dtype."""
+    _, shape, ws, ss = CASES[0]
+    C = shape[-1]
+    x = seeded(shape, torch.float16, 45)
+    w = (seeded((32, C), torch.float32, 46) / C ** 0.5).to(torch.float16)
+    got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), None, ws, ss, normalize=False)
+    want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), None, normalize=False)
+    _compare(got, want, torch.float16, "no norm, no bias")
+    gw = (seeded((C,), torch.float32, 47) + 1.0).to(torch.float16)
+    got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), None, ws, ss, gw.to(dev), None, 1e-6)
+    want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), None, gw.double().numpy(), None, 1e-6)
+    _compare(got, want, torch.float16, "fp16 LN weight, no LN bias")
+
+
+@pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_window_proj_matches_oracle(oracle, dev, case, cdt):
+    name, shape, ws, ss = case
+    B, D, H, W, C = shape
+    _skip_unsupported(C, cdt)
+    print(f"window_proj {name} {cdt}", flush=True)
+    Dp, Hp, Wp = (-(-n // k) * k for n, k in zip((D, H, W), ws))
+    nwin = B * (Dp // ws[0]) * (Hp // ws[1]) * (Wp // ws[2])
+    win = seeded((nwin, ws[0] * ws[1] * ws[2], C), torch.float32, 50).to(cdt)
+    w = (seeded((C, C), torch.float32, 51) / C ** 0.5).to(cdt)
+    b = (seeded((C,), torch.float32, 52) * 0.1).to(cdt)
+    got = fused_block.window_proj_3d(win.to(dev), w.to(dev), b.to(dev), B, D, H, W, ws, ss)
+    want = oracle.window_proj(win.double().numpy(), B, D, H, W, ws, ss, w.double().numpy(), b.double().numpy(),
+                              NAME[cdt])
+    assert got.shape == want.shape
+    _compare(got, want, cdt, f"window_proj {name}")
+
+
+def test_identity_round_trip_is_exact(dev):
+    """Identity weights, no norm, fp32: proj(qkv(x)) reproduces x bit for bit."""
+    shape, ws, ss = (2, 12, 12, 12, 48), (7, 7, 7), (3, 3, 3)
+    x = seeded(shape, torch.float32, 53).to(dev)
+    eye = torch.eye(48, device=dev)
+    win = fused_block.window_qkv_3d(x, eye, None, ws, ss, normalize=False)
+    back = fused_block.window_proj_3d(win, eye, None, 2, 12, 12, 12, ws, ss)
+    assert torch.equal(back, x)
+
+
+def test_invalid_arguments(dev):
+    x = torch.zeros((1, 7, 7, 7, 24), device=dev)
+    with pytest.raises(RuntimeError, match="multiple of 16"):
+        fused_block.window_qkv_3d(x, torch.zeros((48, 24), device=dev), None, (7, 7, 7), (3, 3, 3))
+    x = torch.zeros((1, 7, 7, 7, 32), device=dev)
+    with pytest.raises(RuntimeError, match="shift_size"):
+        fused_block.window_qkv_3d(x, torch.zeros((48, 32), device=dev), None, (7, 7, 7), (7, 0, 0))
+    with pytest.raises(RuntimeError, match="weight"):
+        fused_block.window_qkv_3d(x, torch.zeros((48, 16), device=dev), None, (7, 7, 7), (3, 3, 3))
+    empty = fused_block.window_qkv_3d(torch.zeros((0, 7, 7, 7, 32), device=dev),
+                                      torch.zeros((48, 32), device=dev), None, (7, 7, 7), (3, 3, 3))
+    assert empty.shape == (0, 343, 48)
+
+
+@pytest.mark.parametrize("autocast", [False, True], ids=["fp32", "fp16-autocast"])
+@pytest.mark.parametrize("dims,dim,heads,shift", [((12, 12, 12), 48, 3, 3), ((14, 14, 14), 96, 6, 3),
+                                                  ((6, 6, 6), 384, 24, 0)])
+def test_fused_forward_part1_matches_eager(dev, dims, dim, heads, shift, autocast):
+    """The fused forward_part1 against the eager block's own forward_part1 with
+    the MONAI mask (tensor path) and with the geometry (region path)."""
+    torch.manual_seed(60)
+    blk = sw.SwinTransformerBlock(dim=dim, num_heads=heads, window_size=(7, 7, 7),
+                                  shift_size=(shift,) * 3).to(dev).eval()
+    g = torch.Generator().manual_seed(61)
+    x = torch.randn((2,) + dims + (dim,), generator=g).to(dev)
+    ws, ss = sw.get_window_size(dims, blk.window_size, blk.shift_size)
+    padded = tuple(-(-n // k) * k for n, k in zip(dims, ws))
+    mask = sw.compute_mask(padded, ws, ss, dev) if any(s > 0 for s in ss) else None
+
+    cdt = torch.float16 if autocast else torch.float32
+    es = torch.empty((), dtype=cdt).element_size()
+    if 64 * (dim + 16 // es) * es > 64 * 1024:  # C=384 in fp32: the patch keeps the unfused path
+        with torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+            assert not monai_patch._fused_block_supported(blk, x)
+        pytest.skip(f"C={dim} in {cdt} exceeds the staging tile (unfused path)")
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+        want = blk.forward_part1(x, mask).float()
+        assert monai_patch._fused_block_supported(blk, x)
+        got = monai_patch._fused_block_forward(blk, x, mask, sw).float()
+        if mask is not None:
+            setattr(mask, monai_patch._GEOMETRY_ATTR, (*padded, tuple(ws), tuple(ss)))
+            got_region = monai_patch._fused_block_forward(blk, x, mask, sw).float()
+            assert torch.equal(got_region, got) or (got_region - got).abs().max().item() < 1e-3
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    print(f"forward_part1 {dims} C={dim} autocast={autocast}: max-abs {err:.2e} (max {scale:.2f})", flush=True)
+    assert err < (1e-2 * scale if autocast else 1e-4 * max(1.0, scale))

@@ -13,6 +13,11 @@ window grid, the 6^3 stage with window 6 and no shift):
 * fp16 autocast: eager rounds the scores to fp16 before adding the bias,
   the kernel keeps them in fp32, so the bound is 1e-2 relative to the
   largest activation.
+
+Each model-level test runs twice: through the fused block projections
+(norm1 + pad + shift + partition + qkv, and proj + reverse + crop, as
+kernels) and through the partition / attention / unpartition path with
+torch's LayerNorm and Linear layers (CRUMPET_DISABLE_FUSED_BLOCK=1).
 """
 
 from __future__ import annotations
@@ -45,10 +50,18 @@ def _layer(dim, heads, seed, depth=2):
                          qkv_bias=True, downsample=None)
 
 
+@pytest.fixture(params=["fused-block", "unfused-block"])
+def block_mode(request, monkeypatch):
+    """Run a test through the fused block projections and through the
+    partition / attention / unpartition path."""
+    monkeypatch.setenv("CRUMPET_DISABLE_FUSED_BLOCK", "0" if request.param == "fused-block" else "1")
+    return request.param
+
+
 @pytest.mark.parametrize("dims,dim,heads", [((12, 12, 12), 48, 3),   # padded to 14^3, shifted
                                             ((14, 14, 14), 96, 6),   # no padding, shifted
                                             ((6, 6, 6), 384, 24)])   # window 6, no shift (N=216)
-def test_patched_basic_layer_matches_eager_fp32(patched, dev, dims, dim, heads):
+def test_patched_basic_layer_matches_eager_fp32(patched, dev, dims, dim, heads, block_mode):
     layer = _layer(dim, heads, 0).to(dev).eval()
     g = torch.Generator().manual_seed(1)
     x = torch.randn((2, dim) + dims, generator=g).to(dev)
@@ -60,7 +73,7 @@ def test_patched_basic_layer_matches_eager_fp32(patched, dev, dims, dim, heads):
     assert err < 1e-4
 
 
-def test_patched_basic_layer_fp16_autocast(patched, dev):
+def test_patched_basic_layer_fp16_autocast(patched, dev, block_mode):
     layer = _layer(48, 3, 2).to(dev).eval()
     g = torch.Generator().manual_seed(3)
     x = torch.randn((2, 48, 12, 12, 12), generator=g).to(dev)
@@ -73,21 +86,32 @@ def test_patched_basic_layer_fp16_autocast(patched, dev):
     assert err < 1e-2 * scale
 
 
-def test_region_mode_reads_no_mask(patched, dev, monkeypatch):
-    """A shifted block under the patched BasicLayer takes the geometry path."""
+@pytest.mark.parametrize("fused_block_on", [True, False], ids=["fused-block", "unfused-block"])
+def test_region_mode_reads_no_mask(patched, dev, monkeypatch, fused_block_on):
+    """A shifted block under the patched BasicLayer takes the geometry path,
+    with and without the fused block projections."""
+    from crumpet_amd import fused_block
+
+    monkeypatch.setenv("CRUMPET_DISABLE_FUSED_BLOCK", "0" if fused_block_on else "1")
     calls = []
-    real = monai_patch.fused_swin_attention_windows
+    for mod in (monai_patch, fused_block):
+        real_w, real_s = mod.fused_swin_attention_windows, mod.fused_swin_attention_shifted
 
-    def spy(q, k, v, bias, mask, boundary, scale, out):
-        calls.append(mask is not None)
-        return real(q, k, v, bias, mask, boundary, scale, out)
+        def spy_w(q, k, v, bias, mask, boundary, scale, out, _real=real_w):
+            calls.append("tensor" if mask is not None else "none")
+            return _real(q, k, v, bias, mask, boundary, scale, out)
 
-    monkeypatch.setattr(monai_patch, "fused_swin_attention_windows", spy)
+        def spy_s(*args, _real=real_s, **kw):
+            calls.append("region")
+            return _real(*args, **kw)
+
+        monkeypatch.setattr(mod, "fused_swin_attention_windows", spy_w)
+        monkeypatch.setattr(mod, "fused_swin_attention_shifted", spy_s)
     layer = _layer(48, 3, 4).to(dev).eval()
     x = torch.randn((1, 48, 14, 14, 14), device=dev)
     assert crumpet_amd.patch_monai_swin_unetr()
     _run(layer, x)
-    assert calls == [False]  # block 0 (no shift) only; block 1 used the shifted entry point
+    assert calls == ["none", "region"]  # block 0 has no shift; block 1 reads no mask
 
 
 def test_block_with_foreign_mask_uses_tensor_mask(patched, dev):
@@ -104,7 +128,7 @@ def test_block_with_foreign_mask_uses_tensor_mask(patched, dev):
     assert err < 1e-4
 
 
-def test_patched_swin_unetr_matches_eager_fp32(patched, dev):
+def test_patched_swin_unetr_matches_eager_fp32(patched, dev, block_mode):
     torch.manual_seed(7)
     model = sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=48).to(dev).eval()
     g = torch.Generator().manual_seed(8)
