@@ -290,7 +290,7 @@ def bench_fused_block(args, dev):
     import torch
 
     import crumpet_amd
-    from crumpet_amd import fused_block, monai_patch
+    from crumpet_amd import monai_patch
     from crumpet_amd import swin_unetr_compat as sw
 
     res = {}
@@ -343,10 +343,10 @@ def bench_fused_block(args, dev):
         win = seeded((B * nw, n, C), torch.float16, 720 + dim).to(dev)
         y = torch.empty((B, dim, dim, dim, C), dtype=torch.float16, device=dev)
         nrm = blk.norm1
-        t_qkv = _events_time(lambda i: fused_block.window_qkv_3d(
-            x, w_qkv, b_qkv, ws, ss, nrm.weight, nrm.bias, nrm.eps, True, torch.float16, qkv_out), args.steps)
-        t_proj = _events_time(lambda i: fused_block.window_proj_3d(
-            win, w_p, b_p, B, dim, dim, dim, ws, ss, y), args.steps)
+        ops = torch.ops.crumpet_ops  # raw ops: no wrapper overhead between launches
+        t_qkv = _events_time(lambda i: ops.window_qkv_3d(
+            qkv_out, x, nrm.weight, nrm.bias, nrm.eps, True, w_qkv, b_qkv, *ws, *ss), args.steps)
+        t_proj = _events_time(lambda i: ops.window_proj_3d(y, win, w_p, b_p, *ws, *ss), args.steps)
         qkv_bytes = x.numel() * 4 + qkv_out.numel() * 2
         proj_bytes = win.numel() * 2 + y.numel() * 2
         gq = qkv_bytes / (t_qkv * 1e-3) / 1e9
@@ -496,6 +496,30 @@ def profile_run(dev):
     for i in range(n):
         t = qkvs[i % 3].reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4)
         fused_swin_attention_shifted(t[0], t[1], t[2], bias, vol, (7, 7, 7), (3, 3, 3), 0.25, ov)
+    torch.cuda.synchronize()
+    del qkvs, o, ov, mask
+
+    # fused block projections at the config-5 stage-0 shape: fp32 block
+    # input [4,48^3,48] -> fp16 qkv [1372,343,144]; fp16 attention output
+    # [1372,343,48] -> fp16 block output [4,48^3,48]; 2 rotating sets
+    from crumpet_amd import fused_block
+
+    C0 = 48
+    xs = [seeded((4, 48, 48, 48, C0), torch.float32, 130 + r).to(dev) for r in range(2)]
+    gw = torch.ones(C0, device=dev)
+    gb = torch.zeros(C0, device=dev)
+    wq = (seeded((3 * C0, C0), torch.float32, 134) / C0 ** 0.5).half().to(dev)
+    bq = torch.zeros(3 * C0, dtype=torch.float16, device=dev)
+    qouts = [torch.empty((1372, 343, 3 * C0), dtype=torch.float16, device=dev) for _ in range(2)]
+    for i in range(n):
+        fused_block.window_qkv_3d(xs[i % 2], wq, bq, (7, 7, 7), (3, 3, 3), gw, gb, 1e-5, True, torch.float16,
+                                  qouts[i % 2])
+    del xs, qouts
+    wins = [seeded((1372, 343, C0), torch.float16, 135 + r).to(dev) for r in range(2)]
+    wp = (seeded((C0, C0), torch.float32, 137) / C0 ** 0.5).half().to(dev)
+    ys = [torch.empty((4, 48, 48, 48, C0), dtype=torch.float16, device=dev) for _ in range(2)]
+    for i in range(n):
+        fused_block.window_proj_3d(wins[i % 2], wp, None, 4, 48, 48, 48, (7, 7, 7), (3, 3, 3), ys[i % 2])
     torch.cuda.synchronize()
     print("profile sequence done", flush=True)
 

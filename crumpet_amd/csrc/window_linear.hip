@@ -34,6 +34,8 @@
 // accumulated in fp32, the bias added in fp32, one rounding at the store.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "crumpet_common.h"
 #include "crumpet_hip.h"
 
@@ -156,38 +158,92 @@ __device__ __forceinline__ f32x4 load_param4(const void* p, int32_t dtype, int c
     return load4(static_cast<const __bf16*>(p) + c);
 }
 
-// GEMM over the staged tile: out^T[f][t] = sum_k W[f][k] a[t][k] (+ bias[f]).
-// Wave w takes feature tiles w, w+4, ...; lane (col = l % 16, g = l / 16)
-// ends with features 16 ft + 4g .. +3 of token 16 s + col for s = 0..3 and
-// hands them to `store(token_in_tile, feature, values)`.
-template <typename Tc, typename Store>
-__device__ __forceinline__ void tile_gemm(const Tc* __restrict__ a_lds, int stride, const Tc* __restrict__ w,
-                                          const Tc* __restrict__ bias, int C, int n_out, Store store) {
+// Launch shape shared by both kernels (host-computed).
+struct TileShape {
+    int32_t C, n_out;
+    int32_t fchunk;   // features per LDS output chunk (multiple of 16)
+    int32_t fgroup;   // features per workgroup along grid y (multiple of fchunk)
+    int32_t astride;  // LDS row stride of the input tile (elements)
+    int32_t ostride;  // LDS row stride of the output chunk (elements)
+};
+
+// GEMM over the staged tile and a coalesced store of the result:
+//   out^T[f][t] = sum_k W[f][k] a[t][k] + bias[f]
+// for this workgroup's features [f_begin, f_end), in chunks of fchunk.
+// Per chunk, wave w takes the 16-feature tiles w, w+4, ...; each tile's
+// weight fragments (from L2) are requested before its MFMAs.  Lane (col, g)
+// ends with features 4g..4g+3 of token 16 s + col, which go to the LDS
+// output chunk.  (Requesting the next tile's fragments during the current
+// one measured slower: the extra registers cost occupancy.)  After a barrier the 256 threads write the chunk as
+// 16-byte vectors, row by row: row r of the tile goes to element offset
+// rows_lds[r] * n_out (rows_lds[r] < 0: not stored).
+template <typename Tc, int kKSteps>
+__device__ __forceinline__ void gemm_store(const Tc* __restrict__ a_lds, Tc* __restrict__ o_lds,
+                                           const int32_t* __restrict__ rows_lds, const Tc* __restrict__ w,
+                                           const Tc* __restrict__ bias, Tc* __restrict__ out,
+                                           const TileShape& ts, int f_begin, int f_end) {
     typedef typename Mma<Tc>::x4 X4;
+    typedef Tc T8 __attribute__((ext_vector_type(16 / sizeof(Tc))));
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int col = lane & 15;
     const int g = lane >> 4;
+    const int C = ts.C;
     const int ksteps = C >> 4;
-    for (int ft = wave; ft < (n_out >> 4); ft += 4) {
-        const Tc* wrow = w + int64_t(16 * ft + col) * C + 4 * g;
-        f32x4 acc[4];
+    constexpr int kEpv = 16 / sizeof(Tc);  // elements per 16-byte vector
+    for (int c0 = f_begin; c0 < f_end; c0 += ts.fchunk) {
+        const int c1 = min(f_end, c0 + ts.fchunk);
+        for (int ft = (c0 >> 4) + wave; ft < (c1 >> 4); ft += 4) {
+            const Tc* wrow = w + int64_t(16 * ft + col) * C + 4 * g;
+            X4 wf[kKSteps];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        for (int kk = 0; kk < ksteps; ++kk) {
-            const X4 wf = *reinterpret_cast<const X4*>(wrow + 16 * kk);
+            for (int kk = 0; kk < kKSteps; ++kk)
+                if (kk < ksteps) wf[kk] = *reinterpret_cast<const X4*>(wrow + 16 * kk);
+            const int f0 = 16 * ft + 4 * g;
+            const f32x4 b4 = bias ? load4(bias + f0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            f32x4 acc[4];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const X4 bf = *reinterpret_cast<const X4*>(&a_lds[(16 * s + col) * stride + 16 * kk + 4 * g]);
-                acc[s] = Mma<Tc>::step(wf, bf, acc[s]);
+            for (int s = 0; s < 4; ++s) acc[s] = b4;
+#pragma unroll
+            for (int kk = 0; kk < kKSteps; ++kk) {
+                if (kk < ksteps) {
+#pragma unroll
+                    for (int s = 0; s < 4; ++s) {
+                        const X4 bf =
+                            *reinterpret_cast<const X4*>(&a_lds[(16 * s + col) * ts.astride + 16 * kk + 4 * g]);
+                        acc[s] = Mma<Tc>::step(wf[kk], bf, acc[s]);
+                    }
+                }
             }
-        }
-        const int f0 = 16 * ft + 4 * g;
-        const f32x4 b4 = bias ? load4(bias + f0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) store(16 * s + col, f0, acc[s] + b4);
+            for (int s = 0; s < 4; ++s) store4(&o_lds[(16 * s + col) * ts.ostride + (f0 - c0)], acc[s]);
+        }
+        __syncthreads();
+        const int vpr = (c1 - c0) / kEpv;  // vectors per row of this chunk
+        for (int i = threadIdx.x; i < kTileTokens * vpr; i += kThreads) {
+            const int r = i / vpr;
+            const int j = i - r * vpr;
+            const int32_t row = rows_lds[r];
+            if (row >= 0)
+                __builtin_nontemporal_store(*reinterpret_cast<const T8*>(&o_lds[r * ts.ostride + j * kEpv]),
+                                            reinterpret_cast<T8*>(out + int64_t(row) * ts.n_out + c0 + j * kEpv));
+        }
+        if (c1 < f_end) __syncthreads();  // the next chunk reuses o_lds
     }
 }
+
+// Dynamic LDS of a tile: input rows, output chunk, 64 output row indices.
+template <typename Tc>
+struct TileLds {
+    Tc* a;
+    Tc* o;
+    int32_t* rows;
+    __device__ __forceinline__ TileLds(unsigned char* smem, const TileShape& ts) {
+        a = reinterpret_cast<Tc*>(smem);
+        o = a + kTileTokens * ts.astride;
+        rows = reinterpret_cast<int32_t*>(o + kTileTokens * ts.ostride);
+    }
+};
 
 // LN + pad + shift + partition + qkv projection.  kCpl: 4-element chunks of
 // a token row held per lane (4 lanes per token), C <= 16 * kCpl.
@@ -195,11 +251,18 @@ template <typename Tx, typename Tc, int kCpl>
 __global__ void __launch_bounds__(kThreads)
 window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln_w, const void* ln_b,
                   int32_t ln_dtype, int32_t normalize, float eps, const Tc* __restrict__ w,
-                  const Tc* __restrict__ bias, int32_t C, int32_t n_out, const WinGeom g) {
+                  const Tc* __restrict__ bias, const TileShape ts, const WinGeom g) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    Tc* a_lds = reinterpret_cast<Tc*>(smem);
-    const int stride = C + row_pad<Tc>();
+    const TileLds<Tc> L(smem, ts);
+    const int C = ts.C;
     const uint32_t t0 = blockIdx.x * kTileTokens;
+    const int f_begin = blockIdx.y * ts.fgroup;
+    const int f_end = min(ts.n_out, f_begin + ts.fgroup);
+    if (threadIdx.x < kTileTokens) {
+        // the tile's qkv rows are consecutive
+        const uint32_t t = t0 + threadIdx.x;
+        L.rows[threadIdx.x] = t < g.tokens ? static_cast<int32_t>(t) : -1;
+    }
     {
         // 16 tokens per wave, 4 lanes per token; lane part p holds the
         // chunks p, p + 4, ... (channels 4c .. 4c + 3 of chunk c)
@@ -252,25 +315,30 @@ window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln
 #pragma unroll
         for (int j = 0; j < kCpl; ++j) {
             const int c = part + 4 * j;
-            if (c < nch) store4(&a_lds[tl * stride + 4 * c], v[j]);
+            if (c < nch) store4(&L.a[tl * ts.astride + 4 * c], v[j]);
         }
     }
     __syncthreads();
-    tile_gemm<Tc>(a_lds, stride, w, bias, C, n_out, [&](int tl, int f0, f32x4 r) {
-        const uint32_t t = t0 + tl;
-        if (t < g.tokens) store4(out + int64_t(t) * n_out + f0, r);
-    });
+    gemm_store<Tc, kCpl>(L.a, L.o, L.rows, w, bias, out, ts, f_begin, f_end);
 }
 
 // proj projection + inverse partition + reverse shift + crop.
-template <typename Tc>
+template <typename Tc, int kKSteps>
 __global__ void __launch_bounds__(kThreads)
 window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __restrict__ w,
-                   const Tc* __restrict__ bias, int32_t C, int32_t n_out, const WinGeom g) {
+                   const Tc* __restrict__ bias, const TileShape ts, const WinGeom g) {
     extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-    Tc* a_lds = reinterpret_cast<Tc*>(smem);
-    const int stride = C + row_pad<Tc>();
+    const TileLds<Tc> L(smem, ts);
+    const int C = ts.C;
     const uint32_t t0 = blockIdx.x * kTileTokens;
+    const int f_begin = blockIdx.y * ts.fgroup;
+    const int f_end = min(ts.n_out, f_begin + ts.fgroup);
+    if (threadIdx.x < kTileTokens) {
+        // volume row of each token (the scatter); padding and the tail: none
+        const uint32_t t = t0 + threadIdx.x;
+        const uint32_t row = t < g.tokens ? token_row(t, g) : kPadRow;
+        L.rows[threadIdx.x] = row == kPadRow ? -1 : static_cast<int32_t>(row);
+    }
     // the tile's 64 window-ordered rows are contiguous: 4-element chunks
     const int nch = C >> 2;
     const uint32_t rows = min(uint32_t(kTileTokens), g.tokens - t0);
@@ -280,15 +348,10 @@ window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __r
         const int c = i - r * nch;
         f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if (uint32_t(r) < rows) v = load4(src + int64_t(r) * C + 4 * c);
-        store4(&a_lds[r * stride + 4 * c], v);
+        store4(&L.a[r * ts.astride + 4 * c], v);
     }
     __syncthreads();
-    tile_gemm<Tc>(a_lds, stride, w, bias, C, n_out, [&](int tl, int f0, f32x4 r) {
-        const uint32_t t = t0 + tl;
-        if (t >= g.tokens) return;
-        const uint32_t row = token_row(t, g);
-        if (row != kPadRow) store4(y + int64_t(row) * n_out + f0, r);
-    });
+    gemm_store<Tc, kKSteps>(L.a, L.o, L.rows, w, bias, y, ts, f_begin, f_end);
 }
 
 int elem_size(int32_t dtype) {
@@ -332,32 +395,59 @@ int make_geometry(const char* what, int64_t B, int64_t D, int64_t H, int64_t W, 
     return CRUMPET_OK;
 }
 
-int check_linear(const char* what, int64_t C, int64_t n_out, int32_t dtype, const void* weight) {
+// Validates the projection and plans its tile: the LDS output chunk is as
+// wide as fits next to the staged input rows (at most 192 16-bit or 96 fp32
+// features), and small token counts split the features over grid y so that
+// the launch still covers the chip.
+int plan_tile(const char* what, int64_t C, int64_t n_out, int32_t dtype, const void* weight, uint32_t tokens,
+              TileShape& ts, size_t& lds, dim3& grid) {
     if (C <= 0 || C % 16 != 0)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: channels (%lld) must be a positive multiple of 16",
                     what, (long long)C);
-    if (n_out <= 0 || n_out % 16 != 0)
-        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: output features (%lld) must be a positive multiple of 16",
-                    what, (long long)n_out);
-    if (elem_size(dtype) == 0)
-        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported compute dtype %d", what, dtype);
+    if (C > 16 * 24) return fail(CRUMPET_ERR_UNSUPPORTED, "%s: at most 384 channels", what);
+    if (n_out <= 0 || n_out % 16 != 0 || n_out > (int64_t(1) << 20))
+        return fail(CRUMPET_ERR_UNSUPPORTED,
+                    "%s: output features (%lld) must be a positive multiple of 16 (at most 2^20)", what,
+                    (long long)n_out);
+    const int es = elem_size(dtype);
+    if (es == 0) return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported compute dtype %d", what, dtype);
     if (weight == nullptr) return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: null weight", what);
-    const int64_t lds = int64_t(kTileTokens) * (C + 16 / elem_size(dtype)) * elem_size(dtype);
-    if (lds > kMaxLdsBytes)
+    const int pad = 16 / es;
+    const int64_t a_bytes = int64_t(kTileTokens) * (C + pad) * es;
+    const int64_t rows_bytes = int64_t(kTileTokens) * 4;
+    int fchunk = static_cast<int>(std::min<int64_t>(n_out, es == 2 ? 192 : 96));
+    while (fchunk >= 16 && a_bytes + int64_t(kTileTokens) * (fchunk + pad) * es + rows_bytes > kMaxLdsBytes)
+        fchunk -= 16;
+    if (fchunk < 16)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: %lld channels of %d bytes exceed the staging tile",
-                    what, (long long)C, elem_size(dtype));
+                    what, (long long)C, es);
+    const uint32_t tiles = (tokens + kTileTokens - 1) / kTileTokens;
+    const int nft = static_cast<int>(n_out / 16);
+    int groups = static_cast<int>(std::min<int64_t>(std::max<int64_t>(1, (1024 + tiles - 1) / std::max(tiles, 1u)),
+                                                    std::max(1, nft / 4)));
+    const int fgroup = (nft + groups - 1) / groups * 16;
+    groups = static_cast<int>((n_out + fgroup - 1) / fgroup);
+    ts.C = static_cast<int32_t>(C);
+    ts.n_out = static_cast<int32_t>(n_out);
+    ts.fgroup = fgroup;
+    ts.fchunk = std::min(fchunk, fgroup);
+    ts.astride = static_cast<int32_t>(C) + pad;
+    ts.ostride = ts.fchunk + pad;
+    lds = static_cast<size_t>(a_bytes + int64_t(kTileTokens) * ts.ostride * es + rows_bytes);
+    grid = dim3(tiles, groups);
     return CRUMPET_OK;
 }
 
 template <typename Tx, typename Tc>
-void launch_qkv(int cpl, dim3 grid, size_t lds, hipStream_t s, void* out, const void* x,
-                const void* ln_w, const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps,
-                const void* w, const void* bias, int32_t C, int32_t n_out, const WinGeom& g) {
+void launch_qkv(dim3 grid, size_t lds, hipStream_t s, void* out, const void* x, const void* ln_w,
+                const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps, const void* w,
+                const void* bias, const TileShape& ts, const WinGeom& g) {
 #define CRUMPET_QKV(K)                                                                            \
     hipLaunchKernelGGL((window_qkv_kernel<Tx, Tc, K>), grid, dim3(kThreads), lds, s,             \
                        static_cast<Tc*>(out), static_cast<const Tx*>(x), ln_w, ln_b, ln_dtype,  \
                        normalize, eps, static_cast<const Tc*>(w), static_cast<const Tc*>(bias), \
-                       C, n_out, g)
+                       ts, g)
+    const int cpl = ts.C / 16;
     if (cpl <= 3)
         CRUMPET_QKV(3);
     else if (cpl <= 6)
@@ -370,18 +460,34 @@ void launch_qkv(int cpl, dim3 grid, size_t lds, hipStream_t s, void* out, const 
 }
 
 template <typename Tx>
-void launch_qkv_x(int32_t dtype, int cpl, dim3 grid, size_t lds, hipStream_t s, void* out,
-                  const void* x, const void* ln_w, const void* ln_b, int32_t ln_dtype, int32_t normalize,
-                  float eps, const void* w, const void* bias, int32_t C, int32_t n_out, const WinGeom& g) {
+void launch_qkv_x(int32_t dtype, dim3 grid, size_t lds, hipStream_t s, void* out, const void* x,
+                  const void* ln_w, const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps,
+                  const void* w, const void* bias, const TileShape& ts, const WinGeom& g) {
     if (dtype == CRUMPET_DTYPE_F16)
-        launch_qkv<Tx, _Float16>(cpl, grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias,
-                                 C, n_out, g);
+        launch_qkv<Tx, _Float16>(grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, ts, g);
     else if (dtype == CRUMPET_DTYPE_BF16)
-        launch_qkv<Tx, __bf16>(cpl, grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias,
-                               C, n_out, g);
+        launch_qkv<Tx, __bf16>(grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, ts, g);
     else
-        launch_qkv<Tx, float>(cpl, grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias,
-                              C, n_out, g);
+        launch_qkv<Tx, float>(grid, lds, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, ts, g);
+}
+
+template <typename Tc>
+void launch_proj(dim3 grid, size_t lds, hipStream_t s, void* y, const void* win, const void* w,
+                 const void* bias, const TileShape& ts, const WinGeom& g) {
+#define CRUMPET_PROJ(K)                                                                           \
+    hipLaunchKernelGGL((window_proj_kernel<Tc, K>), grid, dim3(kThreads), lds, s, static_cast<Tc*>(y), \
+                       static_cast<const Tc*>(win), static_cast<const Tc*>(w),                   \
+                       static_cast<const Tc*>(bias), ts, g)
+    const int ks = ts.C / 16;
+    if (ks <= 3)
+        CRUMPET_PROJ(3);
+    else if (ks <= 6)
+        CRUMPET_PROJ(6);
+    else if (ks <= 12)
+        CRUMPET_PROJ(12);
+    else
+        CRUMPET_PROJ(24);
+#undef CRUMPET_PROJ
 }
 
 }  // namespace
@@ -399,12 +505,13 @@ extern "C" int crumpet_window_qkv_3d(void* out, int32_t dtype, const void* x, in
     WinGeom g;
     int st = make_geometry(what, B, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, g);
     if (st != CRUMPET_OK) return st;
-    st = check_linear(what, C, n_out, dtype, weight);
+    TileShape ts;
+    size_t lds;
+    dim3 grid;
+    st = plan_tile(what, C, n_out, dtype, weight, g.tokens, ts, lds, grid);
     if (st != CRUMPET_OK) return st;
     if (elem_size(x_dtype) == 0)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported input dtype %d", what, x_dtype);
-    if (C > 16 * 24)
-        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: at most 384 channels", what);
     if (normalize && (ln_weight || ln_bias) && ln_dtype != CRUMPET_DTYPE_F32 && ln_dtype != x_dtype)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT,
                     "%s: LayerNorm parameters must be float32 or the input dtype", what);
@@ -417,21 +524,16 @@ extern "C" int crumpet_window_qkv_3d(void* out, int32_t dtype, const void* x, in
          reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
          reinterpret_cast<uintptr_t>(ln_weight) | reinterpret_cast<uintptr_t>(ln_bias)) % 16 != 0)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: pointers must be 16-byte aligned", what);
-    const int es = elem_size(dtype);
-    const size_t lds = size_t(kTileTokens) * (C + 16 / es) * es;
-    const dim3 grid((g.tokens + kTileTokens - 1) / kTileTokens);
-    const int cpl = static_cast<int>(C / 16);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int32_t ci = static_cast<int32_t>(C), no = static_cast<int32_t>(n_out);
     if (x_dtype == CRUMPET_DTYPE_F32)
-        launch_qkv_x<float>(dtype, cpl, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
-                            weight, bias, ci, no, g);
+        launch_qkv_x<float>(dtype, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps, weight,
+                            bias, ts, g);
     else if (x_dtype == CRUMPET_DTYPE_F16)
-        launch_qkv_x<_Float16>(dtype, cpl, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize,
-                               eps, weight, bias, ci, no, g);
+        launch_qkv_x<_Float16>(dtype, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                               weight, bias, ts, g);
     else
-        launch_qkv_x<__bf16>(dtype, cpl, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize,
-                             eps, weight, bias, ci, no, g);
+        launch_qkv_x<__bf16>(dtype, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps, weight,
+                             bias, ts, g);
     return check_launch(what);
 }
 
@@ -444,7 +546,10 @@ extern "C" int crumpet_window_proj_3d(void* y, const void* windows, int32_t dtyp
     WinGeom g;
     int st = make_geometry(what, B, D, H, W, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w, g);
     if (st != CRUMPET_OK) return st;
-    st = check_linear(what, C, n_out, dtype, weight);
+    TileShape ts;
+    size_t lds;
+    dim3 grid;
+    st = plan_tile(what, C, n_out, dtype, weight, g.tokens, ts, lds, grid);
     if (st != CRUMPET_OK) return st;
     if (g.tokens == 0) return CRUMPET_OK;
     if (y == nullptr || windows == nullptr)
@@ -452,21 +557,12 @@ extern "C" int crumpet_window_proj_3d(void* y, const void* windows, int32_t dtyp
     if ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(windows) |
          reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias)) % 16 != 0)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: pointers must be 16-byte aligned", what);
-    const int es = elem_size(dtype);
-    const size_t lds = size_t(kTileTokens) * (C + 16 / es) * es;
-    const dim3 grid((g.tokens + kTileTokens - 1) / kTileTokens);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int32_t ci = static_cast<int32_t>(C), no = static_cast<int32_t>(n_out);
-#define CRUMPET_PROJ(T)                                                                           \
-    hipLaunchKernelGGL((window_proj_kernel<T>), grid, dim3(kThreads), lds, s, static_cast<T*>(y), \
-                       static_cast<const T*>(windows), static_cast<const T*>(weight),            \
-                       static_cast<const T*>(bias), ci, no, g)
     if (dtype == CRUMPET_DTYPE_F16)
-        CRUMPET_PROJ(_Float16);
+        launch_proj<_Float16>(grid, lds, s, y, windows, weight, bias, ts, g);
     else if (dtype == CRUMPET_DTYPE_BF16)
-        CRUMPET_PROJ(__bf16);
+        launch_proj<__bf16>(grid, lds, s, y, windows, weight, bias, ts, g);
     else
-        CRUMPET_PROJ(float);
-#undef CRUMPET_PROJ
+        launch_proj<float>(grid, lds, s, y, windows, weight, bias, ts, g);
     return check_launch(what);
 }

@@ -112,6 +112,24 @@ def test_window_proj_matches_oracle(oracle, dev, case, cdt):
     _compare(got, want, cdt, f"window_proj {name}")
 
 
+def test_many_tiles_uneven_feature_chunks(oracle, dev):
+    """Over 1024 token tiles (no feature split across the grid) and 208
+    output features: two LDS chunks (192 + 16), so three of the four waves
+    have no tile in the second chunk."""
+    shape, ws, ss = (1, 40, 40, 40, 32), (7, 7, 7), (3, 3, 3)
+    x = seeded(shape, torch.float16, 54)
+    w = (seeded((208, 32), torch.float32, 55) / 32 ** 0.5).to(torch.float16)
+    b = (seeded((208,), torch.float32, 56) * 0.1).to(torch.float16)
+    got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), b.to(dev), ws, ss)
+    want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), b.double().numpy())
+    _compare(got, want, torch.float16, "qkv 208 features")
+    y = fused_block.window_proj_3d(got, (seeded((208, 208), torch.float32, 57) / 208 ** 0.5).to(torch.float16).to(dev),
+                                   None, 1, 40, 40, 40, ws, ss)
+    wp = (seeded((208, 208), torch.float32, 57) / 208 ** 0.5).to(torch.float16)
+    want_y = oracle.window_proj(got.double().cpu().numpy(), 1, 40, 40, 40, ws, ss, wp.double().numpy())
+    _compare(y, want_y, torch.float16, "proj 208 features")
+
+
 def test_identity_round_trip_is_exact(dev):
     """Identity weights, no norm, fp32: proj(qkv(x)) reproduces x bit for bit."""
     shape, ws, ss = (2, 12, 12, 12, 48), (7, 7, 7), (3, 3, 3)
