@@ -17,7 +17,7 @@ namespace crumpet {
 namespace {
 
 // Workgroups a call aims for: each walks win_per_wg windows; ~4 per CU.
-constexpr int64_t kTargetWorkgroups = 1024;
+constexpr int64_t kTargetWorkgroups = 1536;
 
 int dtype_size(int32_t dt) {
     switch (dt) {

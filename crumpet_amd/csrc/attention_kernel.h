@@ -70,6 +70,11 @@ namespace attn {
 constexpr int kWaves = 4;  // waves (strips) per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr float kLog2e = 1.4426950408889634f;
+// After the first key chunk of a strip, scores may exceed the running row
+// max by this much (natural-log units) before the max is refreshed: the
+// chunk's exps start right away with the running max, and P = exp(s - m)
+// stays below e^8, well inside fp16 / bf16 range.
+constexpr float kLazyMargin = 8.0f;
 
 // Mask modes (template parameter kMask).
 enum MaskKind { kNoMask = 0, kMaskF16 = 1, kMaskF32 = 2, kMaskBF16 = 3, kMaskRegion = 4 };
@@ -217,10 +222,17 @@ __device__ __forceinline__ typename Frag<T>::x4 zero4() {
     return r;
 }
 
-// Waves per SIMD the register allocation targets: the strip's bias tiles and
-// score row (2 * NT * 4 fp32 per lane) dominate the budget.
-template <int NT>
+// Waves per SIMD the register allocation targets: the strip's fp32 bias
+// tiles (4 * NT per lane) and one chunk of scores dominate the budget.  With
+// 2-byte types and vector IO (K and V arrive by LDS DMA, no staging
+// registers) up to 22 tiles fit 168 VGPRs, i.e. 3 waves; the latency-bound
+// loop gains more from the third wave than it loses to the smaller budget.
+template <typename T, int NT, int kMask, bool kVec>
 constexpr int waves_per_eu() {
+    // (an fp32 mask's prefetch ring needs a few more registers than 168 at
+    // 22 tiles)
+    if constexpr (sizeof(T) == 2 && kVec && !(kMask == kMaskF32 && NT > 14))
+        return NT <= 4 ? 4 : (NT <= 22 ? 3 : 2);
     return NT <= 4 ? 4 : (NT <= 8 ? 3 : 2);
 }
 
@@ -675,15 +687,21 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
         for (int t = 0; t < kPrefetch; ++t) fetch(t, t);
     }
 
-    // Keys are processed in chunks of at most kChunk tiles with an online
-    // softmax between chunks (running max, rescaled O and row sums), which
-    // keeps only one chunk of scores in registers next to the bias tiles.
-    constexpr int kNumChunks = (NT + 11) / 12;
+    // Keys are processed in chunks of at most 6 tiles with an online softmax
+    // between chunks, which keeps only one chunk of scores in registers next
+    // to the bias tiles.  The first chunk sets the row max exactly; a later
+    // chunk exponentiates against the running max unless one of its scores
+    // exceeds it by more than kLazyMargin (a wave-uniform test), in which
+    // case the max is refreshed across the lane groups and O and the row
+    // sums are rescaled first.  Softmax is invariant to the offset, so only
+    // the rare refresh costs a cross-lane reduction.
+    constexpr int kNumChunks = (NT + 5) / 6;
     constexpr int kChunk = (NT + kNumChunks - 1) / kNumChunks;
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
     float lsum = 0.0f;  // fp32 path row sum (VALU)
     float m_run = -INFINITY;
+    float mb_run = 0.0f;  // m_run * log2(e)
     // V^T fragments: transposed layout (fp32) or transpose reads of row-major V
     const T* vrow = v_row_major<T>() ? &vt_lds[(4 * g + (col >> 2)) * 16 + (col & 3) * 4]
                                      : &vt_lds[col * kVtStride + 4 * g];
@@ -730,8 +748,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
             if constexpr (kUseMask) __builtin_amdgcn_sched_barrier(0);  // keep the mask ring
         }
 
-        // chunk row max: two 3-input maxes per tile on two independent chains,
-        // then across the 4 lane groups
+        // lane-local chunk max: two 3-input maxes per tile on two chains
         float m0 = m_run, m1 = -INFINITY;
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
@@ -744,16 +761,21 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
                 m0 = fmaxf(fmaxf(m0, S[u][2]), S[u][3]);
             }
         }
-        float m = fmaxf(m0, m1);
-        m = xmax32(xmax16(m));
-        const float mb = m * kLog2e;
-        if (c0 > 0) {  // rescale what the earlier chunks accumulated
-            const float alpha = __builtin_amdgcn_exp2f(__builtin_fmaf(m_run, kLog2e, -mb));
+        const float lm = fmaxf(m0, m1);
+        if (c0 == 0) {
+            m_run = xmax32(xmax16(lm));
+            mb_run = m_run * kLog2e;
+        } else if (__builtin_amdgcn_ballot_w64(lm > m_run + kLazyMargin) != 0) {
+            const float m = xmax32(xmax16(lm));
+            const float mbn = m * kLog2e;
+            const float alpha = __builtin_amdgcn_exp2f(mb_run - mbn);
             o *= alpha;
             lacc *= alpha;
             lsum *= alpha;
+            m_run = m;
+            mb_run = mbn;
         }
-        m_run = m;
+        const float mb = mb_run;
 
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
@@ -840,7 +862,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
 
 template <typename T, int NT, int kMask, bool kVec>
 __global__ void __launch_bounds__(kThreads)
-__attribute__((amdgpu_waves_per_eu(waves_per_eu<NT>(), waves_per_eu<NT>())))
+__attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask, kVec>(), waves_per_eu<T, NT, kMask, kVec>())))
 swin_attention_d16_kernel(const Params p) {
     typedef Stage<T, NT, kVec> St;
     constexpr int NP = St::NP;
