@@ -78,6 +78,12 @@ def c_abi():
     lib.crumpet_fused_swin_attention_shifted.argtypes = [
         vp, p4, vp, p4, vp, p4, vp, p4, ctypes.c_int32, i64, i64, i64, i64,
         vp, ctypes.c_int32, p4] + [i64] * 9 + [ctypes.c_float, vp]
+    i32, f32 = ctypes.c_int32, ctypes.c_float
+    lib.crumpet_window_qkv_3d.restype = ctypes.c_int
+    lib.crumpet_window_qkv_3d.argtypes = ([vp, i32, vp, i32] + [i64] * 5 + [i32, vp, vp, i32, f32, vp, vp, i64]
+                                          + [i64] * 6 + [vp])
+    lib.crumpet_window_proj_3d.restype = ctypes.c_int
+    lib.crumpet_window_proj_3d.argtypes = [vp, vp, i32] + [i64] * 5 + [vp, vp, i64] + [i64] * 6 + [vp]
     lib.crumpet_last_error.restype = ctypes.c_char_p
     lib.crumpet_status_string.restype = ctypes.c_char_p
     lib.crumpet_status_string.argtypes = [ctypes.c_int]

@@ -96,3 +96,37 @@ def test_c_abi_rejects_bad_arguments(dev):
     assert st == 1 and b"shift" in lib.crumpet_last_error()
     st = lib.crumpet_compute_attn_mask_3d(x.data_ptr(), 9, 14, 14, 14, 7, 7, 7, 3, 3, 3, _stream())
     assert st == 1
+
+
+def test_c_abi_window_projections(oracle, dev):
+    """crumpet_window_qkv_3d / crumpet_window_proj_3d through the raw C ABI:
+    LayerNorm + pad + shift + partition + qkv, then proj + reverse + crop,
+    against the oracle chain (4 ulps of fp16)."""
+    lib = c_abi()
+    B, D, C, ws, ss = 2, 12, 48, (7, 7, 7), (3, 3, 3)
+    x = seeded((B, D, D, D, C), torch.float32, 70)
+    gw = seeded((C,), torch.float32, 71) * 0.5 + 1.0
+    gb = seeded((C,), torch.float32, 72) * 0.1
+    w = (seeded((3 * C, C), torch.float32, 73) / C ** 0.5).half()
+    b = (seeded((3 * C,), torch.float32, 74) * 0.1).half()
+    xd, gwd, gbd, wd, bd = (t.to(dev) for t in (x, gw, gb, w, b))
+    qkv = torch.empty((B * 8, 343, 3 * C), dtype=torch.float16, device=dev)
+    st = lib.crumpet_window_qkv_3d(qkv.data_ptr(), CODE[torch.float16], xd.data_ptr(), CODE[torch.float32],
+                                   B, D, D, D, C, 1, gwd.data_ptr(), gbd.data_ptr(), CODE[torch.float32],
+                                   ctypes.c_float(1e-5), wd.data_ptr(), bd.data_ptr(), 3 * C, *ws, *ss, _stream())
+    assert st == 0, lib.crumpet_last_error()
+    wp = (seeded((C, C), torch.float32, 75) / C ** 0.5).half()
+    wpd = wp.to(dev)
+    y = torch.empty((B, D, D, D, C), dtype=torch.float16, device=dev)
+    win = qkv[:, :, :C].contiguous()
+    st = lib.crumpet_window_proj_3d(y.data_ptr(), win.data_ptr(), CODE[torch.float16], B, D, D, D, C,
+                                    wpd.data_ptr(), None, C, *ws, *ss, _stream())
+    assert st == 0, lib.crumpet_last_error()
+    torch.cuda.synchronize()
+    want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), b.double().numpy(),
+                             gw.double().numpy(), gb.double().numpy(), 1e-5, True, "float16")
+    got = qkv.float().cpu().double().numpy()
+    assert (np.abs(got - want) <= 4 * 2 ** -10 * np.maximum(np.abs(want), 1.0)).all()
+    want_y = oracle.window_proj(win.float().cpu().double().numpy(), B, D, D, D, ws, ss, wp.double().numpy())
+    got_y = y.float().cpu().double().numpy()
+    assert (np.abs(got_y - want_y) <= 4 * 2 ** -10 * np.maximum(np.abs(want_y), 1.0)).all()

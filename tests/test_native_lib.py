@@ -104,6 +104,35 @@ def test_attention_argument_checks_need_no_gpu():
     assert shifted(B=6) == 1 and b"multiple" in lib.crumpet_last_error()
 
 
+def test_window_projection_argument_checks_need_no_gpu():
+    lib = c_abi()
+    fake = ctypes.c_void_p(256)
+    eps = ctypes.c_float(1e-5)
+
+    def qkv(C=48, n_out=144, ws=7, ss=3, x_dtype=0, dtype=1, ln=None, ln_dtype=0, out=fake, B=1):
+        return lib.crumpet_window_qkv_3d(out, dtype, fake, x_dtype, B, 12, 12, 12, C, 1, ln, ln, ln_dtype, eps,
+                                         fake, None, n_out, ws, ws, ws, ss, ss, ss, None)
+
+    assert qkv(C=24) == 2 and b"multiple of 16" in lib.crumpet_last_error()
+    assert qkv(n_out=40) == 2 and b"output features" in lib.crumpet_last_error()
+    assert qkv(C=400) == 2
+    assert qkv(ss=7) == 1 and b"shift_size" in lib.crumpet_last_error()
+    assert qkv(dtype=9) == 1
+    assert qkv(x_dtype=9) == 1
+    assert qkv(ln=fake, ln_dtype=2, x_dtype=1) == 1 and b"LayerNorm" in lib.crumpet_last_error()
+    assert qkv(out=ctypes.c_void_p(8)) == 2 and b"aligned" in lib.crumpet_last_error()
+    assert qkv(dtype=0, C=384, n_out=384) == 2 and b"staging tile" in lib.crumpet_last_error()
+    assert qkv(B=0) == 0  # no tokens: a successful no-op
+
+    def proj(C=48, n_out=48, ws=7, ss=3):
+        return lib.crumpet_window_proj_3d(fake, fake, 1, 1, 12, 12, 12, C, fake, None, n_out,
+                                          ws, ws, ws, ss, ss, ss, None)
+
+    assert proj(C=40) == 2
+    assert proj(n_out=8) == 2
+    assert proj(ws=0) == 1 and b"window_size" in lib.crumpet_last_error()
+
+
 def test_dispatcher_schemas_match_reference():
     import crumpet_amd  # noqa: F401  (loads the binding)
 
