@@ -16,7 +16,10 @@
 namespace crumpet {
 namespace {
 
-// Workgroups a call aims for: each walks win_per_wg windows; ~4 per CU.
+// Workgroups a call aims for: each walks win_per_wg windows.  1536 = two
+// full rounds of 3 resident workgroups on each of the 256 CUs (the 2-byte
+// vector-IO kernels run 3 waves per SIMD); a partial last round costs more
+// than the extra prologues of smaller ranges.
 constexpr int64_t kTargetWorkgroups = 1536;
 
 int dtype_size(int32_t dt) {

@@ -44,10 +44,20 @@
 //   ones^T P^T.  O^T lands as 4 consecutive head-dim values of one query per
 //   lane, which is one 8-byte store.
 //
+// Softmax
+//   Online over key chunks of at most 6 tiles, with a lazy rescale: the
+//   first chunk fixes the row max, later chunks exponentiate against the
+//   running max and refresh it (with a cross-lane reduction and a rescale of
+//   O and the row sums) only when a score exceeds it by more than
+//   kLazyMargin.  The small chunks keep 2-byte vector-IO kernels within 168
+//   VGPRs, i.e. 3 waves per SIMD, which this latency-bound loop needs more
+//   than it needs a larger register budget.
+//
 // Padding
 //   Keys are padded to NP = 16*NT: padded key columns get a -inf bias
 //   (probability exactly 0), padded query rows a 0 bias (never stored).  K, V
-//   and Q rows past N are zero in LDS.  The kernel needs no workspace.
+//   and Q rows past N are copies of row N-1 in LDS (zero on the register
+//   path), harmless under those biases.  The kernel needs no workspace.
 //
 // Numerics follow torch-ext/crumpet/fused_attention.py:82-146: q is scaled
 // in fp32 and rounded back to the input type, products accumulate in fp32,

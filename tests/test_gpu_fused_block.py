@@ -130,6 +130,43 @@ def test_many_tiles_uneven_feature_chunks(oracle, dev):
     _compare(y, want_y, torch.float16, "proj 208 features")
 
 
+def test_stage0_full_size_sampled(oracle, dev):
+    """Config-5 stage 0 at full size ([4,48^3,48] fp32 block input, fp16
+    compute, window 7, shift 3, padded to 49^3): 512 sampled tokens of qkv
+    against the oracle (whose window order is the C oracle's partition), and
+    the proj scatter checked as a permutation of a full-size identity."""
+    B, D, C, ws, ss = 4, 48, 48, (7, 7, 7), (3, 3, 3)
+    x = seeded((B, D, D, D, C), torch.float32, 80) * 1.5 + 0.25
+    gw = seeded((C,), torch.float32, 81) * 0.5 + 1.0
+    gb = seeded((C,), torch.float32, 82) * 0.1
+    w = (seeded((3 * C, C), torch.float32, 83) / C ** 0.5).half()
+    b = (seeded((3 * C,), torch.float32, 84) * 0.1).half()
+    got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), b.to(dev), ws, ss, gw.to(dev), gb.to(dev), 1e-5, True,
+                                    torch.float16)
+    nwin, n = B * 7 ** 3, 343
+    assert got.shape == (nwin, n, 3 * C)
+    # source row of every window-ordered token: partition an index volume
+    # (padded with -1) with the C oracle
+    idx = np.full((B, 49, 49, 49, 1), -1, dtype=np.int32)
+    idx[:, :D, :D, :D, 0] = np.arange(B * D ** 3, dtype=np.int32).reshape(B, D, D, D)
+    src = oracle.shift_partition(idx, ws, ss).reshape(-1)
+    g = np.random.default_rng(85)
+    pick = g.choice(nwin * n, size=512, replace=False)
+    xs = x.reshape(-1, C).double().numpy()
+    rows = np.zeros((512, C))
+    inside = src[pick] >= 0
+    rows[inside] = oracle.round_to(oracle.layer_norm(xs[src[pick][inside]], gw.double().numpy(),
+                                                     gb.double().numpy(), 1e-5), "float16")
+    want = oracle.round_to(rows @ w.double().numpy().T + b.double().numpy(), "float16")
+    _compare(got.reshape(-1, 3 * C)[torch.from_numpy(pick).to(dev)], want, torch.float16, "stage 0 sampled")
+    # proj with identity weights, fp32: the full window -> volume scatter with crop
+    eye = torch.eye(C, device=dev)
+    win = torch.from_numpy(np.where(src >= 0, src, -1).astype(np.float32)).to(dev)[:, None].expand(-1, C)
+    y = fused_block.window_proj_3d(win.reshape(nwin, n, C).contiguous(), eye, None, B, D, D, D, ws, ss)
+    want_y = torch.arange(B * D ** 3, dtype=torch.float32, device=dev)[:, None].expand(-1, C)
+    assert torch.equal(y.reshape(-1, C), want_y)
+
+
 def test_identity_round_trip_is_exact(dev):
     """Identity weights, no norm, fp32: proj(qkv(x)) reproduces x bit for bit."""
     shape, ws, ss = (2, 12, 12, 12, 48), (7, 7, 7), (3, 3, 3)
