@@ -9,7 +9,6 @@ import ctypes
 import re
 from pathlib import Path
 
-import pytest
 import torch
 
 from helpers import c_abi
