@@ -12,7 +12,8 @@ The same run also measures, each on its own BASELINE config:
   * the mask kernel (config 2, 98^3 fp16, 645,657,712 B written);
   * fused window attention (config 3, 1372 windows x 3 heads, N=343, hd 16),
     in TFLOP/s, with the eager ROCm PyTorch chain timed beside it;
-  * the CPU oracle on the host cores as the reported CPU baseline.
+  * the CPU oracle on the host cores as the reported CPU baseline, and each
+    config's eager path on the host cores beside its GPU figure.
 
 Prints ONE JSON line.  Only one GPU is supported: --gpus above 1 exits.
 """
@@ -454,6 +455,113 @@ def cpu_baseline():
             "sample": f"full config-1 round trip ([1,98^3,48] fp16) x{reps}, oracle/crumpet_oracle.c scalar, {el:.1f} s"}
 
 
+def _cpu_median(fn, reps):
+    import statistics
+
+    fn()  # warm
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times)
+
+
+def _cpu_attention(q, k, v, bias, mask, scale):
+    """fp32 eager chain (fused_attention.py:82-146 semantics): q*scale k^T +
+    bias (+ mask) -> softmax -> @ v, on [b, H, N, 16] CPU tensors."""
+    import torch
+
+    s = (q * scale) @ k.transpose(-1, -2) + bias[None]
+    if mask is not None:
+        s = s + mask[:, None]
+    return torch.softmax(s, dim=-1) @ v
+
+
+def cpu_eager_paths(skip_e2e=False):
+    """The reference's eager paths timed on the host cores, one per config,
+    each on a bounded sample stated in its entry (reported baselines only,
+    never targets): torch roll + view/permute (config 1), the two eager mask
+    constructions (config 2), the fp32 attention chain (configs 3 and 4) and
+    the unpatched fp32 Swin UNETR forward (config 5)."""
+    import numpy as np
+    import torch
+
+    from crumpet_amd import swin_unetr_compat as sw
+    from oracle import oracle
+
+    threads = torch.get_num_threads()
+    res = {}
+
+    # config 1: torch.roll + window partition and its inverse, fp16, full volume
+    x = seeded((1, 98, 98, 98, 48), torch.float16, 100)
+
+    def roundtrip():
+        w = sw.window_partition(torch.roll(x, (-3, -3, -3), (1, 2, 3)), (7, 7, 7))
+        torch.roll(sw.window_reverse(w, (7, 7, 7), (1, 98, 98, 98)), (3, 3, 3), (1, 2, 3))
+
+    t = _cpu_median(roundtrip, 3)
+    res["roundtrip"] = {"ms": round(t * 1e3, 2), "GB_s": round(2 * C1_BYTES / t / 1e9, 3), "threads": threads,
+                        "sample": "full config 1, torch.roll + view/permute and the inverse, fp16, "
+                                  "median of 3"}
+    del x
+
+    # config 2: MONAI-style slice construction and the vectorised where, at
+    # D=49 (343 windows, 1/8 of config 2's elements); GB/s of fp16 output
+    n49 = 343 * 343 * 343 * 2
+    t_monai = _cpu_median(lambda: oracle.np_mask_monai_slices(49, 49, 49, (7, 7, 7), (3, 3, 3)).astype(np.float16), 3)
+    t_where = _cpu_median(lambda: np.where(oracle.np_mask_where(49, 49, 49, (7, 7, 7), (3, 3, 3)),
+                                           np.float16(-100), np.float16(0)), 3)
+    res["mask"] = {"ms_monai_slices": round(t_monai * 1e3, 2), "ms_where": round(t_where * 1e3, 2),
+                   "GB_s": round(n49 / min(t_monai, t_where) / 1e9, 3), "threads": 1,
+                   "sample": "D=49 (343 windows x 343^2, 80.7 MB fp16 out), numpy, median of 3"}
+
+    # config 3: fp32 eager attention on every 14th window (98 of 1372)
+    g = torch.Generator().manual_seed(300)
+    qkv = torch.randn((98, 343, 144), generator=g).half().float()
+    t3 = qkv.view(98, 343, 3, 3, 16).permute(2, 0, 3, 1, 4)
+    bias = torch.randn((3, 343, 343), generator=g) * 0.02
+    mask = torch.from_numpy(oracle.attn_mask(49, 49, 49, (7, 7, 7), (3, 3, 3), "float32"))[:98]
+    t = _cpu_median(lambda: _cpu_attention(t3[0], t3[1], t3[2], bias, mask, 0.25), 3)
+    fl = 4 * 343 * 343 * 16 * 3 * 98
+    res["attention"] = {"ms": round(t * 1e3, 2), "TFLOP_s": round(fl / t / 1e12, 4),
+                        "ms_config3_scaled": round(t * 1e3 * 1372 / 98, 1), "threads": threads,
+                        "sample": "98 of the 1372 windows x 3 heads, fp32 torch on CPU, median of 3"}
+    del qkv, t3
+
+    # config 4: partition -> fp32 attention -> unpartition per stage (fp32 math on the fp16 input)
+    for name, dim, C, H, ws, ss in STAGES[:3]:
+        x = seeded((4, dim, dim, dim, C), torch.float16, 500 + dim).float()
+        N = ws[0] * ws[1] * ws[2]
+        b = torch.randn((H, N, N), generator=g) * 0.02
+        m = torch.from_numpy(oracle.attn_mask(dim, dim, dim, ws, ss, "float32")) if any(ss) else None
+
+        def chain():
+            w = sw.window_partition(torch.roll(x, tuple(-s for s in ss), (1, 2, 3)), ws)
+            nw = w.shape[0]
+            t_ = w.view(nw, N, H, 16).permute(0, 2, 1, 3)
+            mm = m.repeat(nw // m.shape[0], 1, 1) if m is not None else None
+            o = _cpu_attention(t_, t_, t_, b, mm, 0.25).permute(0, 2, 1, 3).reshape(nw, N, C)
+            torch.roll(sw.window_reverse(o, ws, (4, dim, dim, dim)), ss, (1, 2, 3))
+
+        res[f"block_path_{name}"] = {"ms": round(_cpu_median(chain, 1) * 1e3, 2), "threads": threads,
+                                     "sample": f"full stage [4,{dim}^3,{C}], fp32, median of 1"}
+
+    # config 5: unpatched fp32 Swin UNETR forward, one sample of the batch of 4
+    if not skip_e2e:
+        torch.manual_seed(123)
+        model = sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=48, depths=(2, 2, 2, 2),
+                             num_heads=(3, 6, 12, 24)).eval()
+        xin = synthetic_ct((1, 1, 96, 96, 96), 77)
+        with torch.no_grad():
+            t = _cpu_median(lambda: model(xin), 1)
+        res["swin_unetr_e2e"] = {"ms_per_sample": round(t * 1e3, 1), "ms_batch4_scaled": round(4 * t * 1e3, 1),
+                                 "threads": threads,
+                                 "sample": "[1,1,96^3] fp32 unpatched eager forward (one of the 4 "
+                                           "samples), median of 1 after a warm-up"}
+    return res
+
+
 def profile_run(dev):
     """Fixed short sequence for rocprofv3: 20 launches of each kernel on
     rotating buffers, plus a plain 256 MiB device copy (read 256 MiB + write
@@ -638,6 +746,16 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        cpu = cpu_eager_paths(skip_e2e=args.no_e2e)
+        components["partition"]["cpu_eager_roundtrip"] = cpu["roundtrip"]
+        components["mask"]["cpu_eager"] = cpu["mask"]
+        if "attention" in components:
+            components["attention"]["cpu_eager"] = cpu["attention"]
+        if blocks:
+            for name in ("s1", "s2", "s3"):
+                blocks[f"cpu_eager_{name}"] = cpu[f"block_path_{name}"]
+        if e2e and "swin_unetr_e2e" in cpu:
+            e2e["cpu_eager"] = cpu["swin_unetr_e2e"]
     line["cpu_baseline_threads"] = {"os_cpu_count": os.cpu_count(),
                                     "torch_threads": torch.get_num_threads()}
     print(json.dumps(line), flush=True)
