@@ -12,7 +12,8 @@
 // the hardware's own workgroup order measured fastest on MI355X for the
 // window-ordered direction (5.8 TB/s for the 98^3 C=48 fp16 partition, 98%
 // of a plain streaming copy); more vectors per thread were slower.  The
-// volume-ordered direction groups workgroups in runs per XCD (3-4% faster).
+// volume-ordered direction groups workgroups in runs per XCD (3-4% faster)
+// and runs 512-thread workgroups (1-2% faster than 256 there).
 //
 // Reference semantics: torch-ext/crumpet/reference.py:141-184 (roll then
 // view/permute, and the inverse); kernels replaced:
@@ -25,8 +26,13 @@
 namespace crumpet {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr uint32_t kXcdRun = 32;  // workgroups per XCD run in the volume-ordered gather
+// Threads per workgroup: 256 for the window-ordered gather, 512 for the
+// volume-ordered one (measured fastest for each at config 1).
+template <bool kToWindows>
+constexpr int threads_for() {
+    return kToWindows ? 256 : 512;
+}
+constexpr uint32_t kXcdRun = 16;  // workgroups per XCD run in the volume-ordered gather
 
 struct GatherGeom {
     uint32_t total;  // output vectors
@@ -104,10 +110,11 @@ __device__ __forceinline__ uint32_t src_for_volume(uint32_t o, const GatherGeom&
 }
 
 template <int VB, bool kToWindows, int U>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(threads_for<kToWindows>())
 window_gather_kernel(typename VecOf<VB>::type* __restrict__ out,
                      const typename VecOf<VB>::type* __restrict__ in, const GatherGeom g) {
     typedef typename VecOf<VB>::type V;
+    constexpr int kThreads = threads_for<kToWindows>();
     uint32_t blk = blockIdx.x;
     if constexpr (!kToWindows) {
         // Volume-ordered output: consecutive rows read the two halves of the
@@ -203,7 +210,8 @@ int launch_gather(bool to_windows, void* out, const void* in, int64_t B, int64_t
     g.f_wsd.init(ws_d);
 
     constexpr int U = 1;
-    const uint32_t blocks = static_cast<uint32_t>((total + kThreads * U - 1) / (kThreads * U));
+    const int threads = to_windows ? threads_for<true>() : threads_for<false>();
+    const uint32_t blocks = static_cast<uint32_t>((total + threads * U - 1) / (threads * U));
     hipStream_t s = static_cast<hipStream_t>(stream);
 
 #define CRUMPET_LAUNCH_GATHER(VBV)                                                           \
@@ -211,11 +219,11 @@ int launch_gather(bool to_windows, void* out, const void* in, int64_t B, int64_t
         typedef typename VecOf<VBV>::type V;                                                 \
         if (to_windows)                                                                      \
             hipLaunchKernelGGL((window_gather_kernel<VBV, true, U>), dim3(blocks),           \
-                               dim3(kThreads), 0, s, static_cast<V*>(out),                   \
+                               dim3(threads), 0, s, static_cast<V*>(out),                   \
                                static_cast<const V*>(in), g);                                \
         else                                                                                 \
             hipLaunchKernelGGL((window_gather_kernel<VBV, false, U>), dim3(blocks),          \
-                               dim3(kThreads), 0, s, static_cast<V*>(out),                   \
+                               dim3(threads), 0, s, static_cast<V*>(out),                   \
                                static_cast<const V*>(in), g);                                \
     } while (0)
 
