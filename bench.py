@@ -563,15 +563,24 @@ def cpu_eager_paths(skip_e2e=False):
 
 
 def profile_run(dev):
-    """Fixed short sequence for rocprofv3: 20 launches of each kernel on
+    """Fixed short sequence for rocprofv3: 2 + 20 launches of each kernel on
     rotating buffers, plus a plain 256 MiB device copy (read 256 MiB + write
-    256 MiB) for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    256 MiB) for scaling the FETCH_SIZE / WRITE_SIZE counters.  Each kernel's
+    last 20 back-to-back launches are timed with one HIP event pair; the last line
+    printed holds the mean per-launch times, so a run without the profiler
+    gives the undisturbed durations of the same launches."""
     import torch
 
     from crumpet_amd.fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
 
     ops = torch.ops.crumpet_ops
     n = 20
+    times = {}
+
+    def timed(name, fn):
+        for i in range(2):  # the first launches load the code object
+            fn(i)
+        times[name] = round(_events_time(fn, n) * 1e3, 2)
     B, D, H, W, C, ws, ss = (C1[k] for k in ("B", "D", "H", "W", "C", "ws", "ss"))
     R = 4
     xs = [seeded((B, D, H, W, C), torch.float16, 100 + r).to(dev) for r in range(R)]
@@ -579,14 +588,12 @@ def profile_run(dev):
     backs = [torch.empty_like(xs[0]) for _ in range(R)]
     src = torch.ones((1 << 27,), dtype=torch.float16, device=dev)
     dst = torch.empty_like(src)
-    for i in range(n):
-        ops.fused_shift_partition_3d(wins[i % R], xs[i % R], *ws, *ss)
-    for i in range(n):
-        ops.fused_unshift_unpartition_3d(backs[i % R], wins[i % R], B, D, H, W, C, *ws, *ss)
+    timed("partition", lambda i: ops.fused_shift_partition_3d(wins[i % R], xs[i % R], *ws, *ss))
+    timed("unpartition",
+          lambda i: ops.fused_unshift_unpartition_3d(backs[i % R], wins[i % R], B, D, H, W, C, *ws, *ss))
     del xs, wins, backs
     outs = [torch.empty((2744, 343, 343), dtype=torch.float16, device=dev) for _ in range(2)]
-    for i in range(n):
-        ops.compute_attn_mask_3d(outs[i % 2], 98, 98, 98, 7, 7, 7, 3, 3, 3)
+    timed("mask", lambda i: ops.compute_attn_mask_3d(outs[i % 2], 98, 98, 98, 7, 7, 7, 3, 3, 3))
     for i in range(10):
         dst.copy_(src)
     torch.cuda.synchronize()
@@ -596,16 +603,15 @@ def profile_run(dev):
     Bw, Hh, N, Dh = C3["B"], C3["H"], C3["N"], C3["Dh"]
     o = torch.empty((Bw, N, Hh * Dh), dtype=torch.float16, device=dev)
     ov = o.view(Bw, N, Hh, Dh).permute(0, 2, 1, 3)
-    for i in range(n):
-        t = qkvs[i % 3].reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4)
-        fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ov)
-    torch.cuda.synchronize()
+    views = [q.reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4) for q in qkvs]
+    timed("attention_tensor_mask",
+          lambda i: fused_swin_attention_windows(views[i % 3][0], views[i % 3][1], views[i % 3][2], bias, mask,
+                                                 bnd, 0.25, ov))
     vol = (C3["D"],) * 3
-    for i in range(n):
-        t = qkvs[i % 3].reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4)
-        fused_swin_attention_shifted(t[0], t[1], t[2], bias, vol, (7, 7, 7), (3, 3, 3), 0.25, ov)
-    torch.cuda.synchronize()
-    del qkvs, o, ov, mask
+    timed("attention_shifted",
+          lambda i: fused_swin_attention_shifted(views[i % 3][0], views[i % 3][1], views[i % 3][2], bias, vol,
+                                                 (7, 7, 7), (3, 3, 3), 0.25, ov))
+    del qkvs, views, o, ov, mask
 
     # fused block projections at the config-5 stage-0 shape: fp32 block
     # input [4,48^3,48] -> fp16 qkv [1372,343,144]; fp16 attention output
@@ -619,17 +625,16 @@ def profile_run(dev):
     wq = (seeded((3 * C0, C0), torch.float32, 134) / C0 ** 0.5).half().to(dev)
     bq = torch.zeros(3 * C0, dtype=torch.float16, device=dev)
     qouts = [torch.empty((1372, 343, 3 * C0), dtype=torch.float16, device=dev) for _ in range(2)]
-    for i in range(n):
-        fused_block.window_qkv_3d(xs[i % 2], wq, bq, (7, 7, 7), (3, 3, 3), gw, gb, 1e-5, True, torch.float16,
-                                  qouts[i % 2])
+    timed("window_qkv", lambda i: fused_block.window_qkv_3d(xs[i % 2], wq, bq, (7, 7, 7), (3, 3, 3), gw, gb, 1e-5,
+                                                            True, torch.float16, qouts[i % 2]))
     del xs, qouts
     wins = [seeded((1372, 343, C0), torch.float16, 135 + r).to(dev) for r in range(2)]
     wp = (seeded((C0, C0), torch.float32, 137) / C0 ** 0.5).half().to(dev)
     ys = [torch.empty((4, 48, 48, 48, C0), dtype=torch.float16, device=dev) for _ in range(2)]
-    for i in range(n):
-        fused_block.window_proj_3d(wins[i % 2], wp, None, 4, 48, 48, 48, (7, 7, 7), (3, 3, 3), ys[i % 2])
-    torch.cuda.synchronize()
+    timed("window_proj", lambda i: fused_block.window_proj_3d(wins[i % 2], wp, None, 4, 48, 48, 48, (7, 7, 7),
+                                                              (3, 3, 3), ys[i % 2]))
     print("profile sequence done", flush=True)
+    print("PROFILE_EVENTS_US " + json.dumps(times), flush=True)
 
 
 def profiled_traffic(name):

@@ -3,8 +3,10 @@
 // The mask [nW, vol, vol] is written as one flat array of 16-byte vectors
 // (8 fp16/bf16 or 4 fp32 elements), so every store is a full, aligned,
 // coalesced 16-byte store, whatever the odd window volume (vol^2 = 117649 at
-// ws=7 leaves the per-window blocks only 2-byte aligned).  Plain stores beat
-// non-temporal ones for this pure write stream on MI355X.
+// ws=7 leaves the per-window blocks only 2-byte aligned).  Each lane writes
+// two adjacent vectors (32 contiguous bytes): on MI355X that write stream
+// runs at the speed of a plain fill, 12% faster than two vectors a
+// workgroup-width apart; plain stores beat non-temporal ones.
 //
 // Which value an element holds follows from two 3-bit codes:
 //   cls[loc]  : for each axis, whether the local coordinate lies at or past
@@ -91,7 +93,7 @@ attn_mask_kernel(u32x4* __restrict__ out, const MaskGeom g) {
     const uint32_t nvec = (g.total_elems + kEpv - 1) / kEpv;
 #pragma unroll
     for (int u = 0; u < kVecPerThread; ++u) {
-        const uint32_t vi = blockIdx.x * (kThreads * kVecPerThread) + u * kThreads + threadIdx.x;
+        const uint32_t vi = (blockIdx.x * kThreads + threadIdx.x) * kVecPerThread + u;
         if (vi >= nvec) break;
         const uint32_t e0 = vi * kEpv;
         uint32_t bits[kEpv];
