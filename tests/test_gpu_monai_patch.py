@@ -155,3 +155,20 @@ def test_training_mode_falls_back_and_backpropagates(patched, dev):
     got.square().mean().backward()
     assert (got - want).abs().max().item() < 1e-4
     assert (x.grad - g_want).abs().max().item() < 1e-5
+
+
+def test_unsupported_head_dim_is_bit_exact_fp16(patched, dev):
+    """tests/test_demo_btcv_smoke.py:37-39 of the reference: with head_dim 4
+    (feature size 12) the fused attention and the fused block are bypassed,
+    the patched model runs the partition / unpartition kernels and the mask
+    kernel around MONAI's own attention, and its fp16 logits equal the eager
+    model's exactly."""
+    torch.manual_seed(10)
+    model = sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=12).to(dev).eval()
+    g = torch.Generator().manual_seed(11)
+    x = torch.rand((1, 1, 64, 64, 64), generator=g).half().to(dev)
+    want = _run(model, x, autocast=True)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(model, x, autocast=True)
+    print(f"hd=4 fp16: max-abs logit delta {(got - want).abs().max().item():.2e}", flush=True)
+    assert torch.equal(got, want)
