@@ -100,8 +100,10 @@ def fused_swin_attention_shifted(
     with ``mask = compute_attn_mask_3d(D, H, W, window_size, shift_size)``
     repeated over the outer batch (window ``b`` uses the mask of window
     ``b % nW``), without materialising, repeating or reading the mask: the
-    kernel adds it from per-window-type bias+mask tables.  ``q``'s batch must
-    be a multiple of ``nW`` and ``N`` the window volume.
+    mask of a window depends only on which axes it is the last window along,
+    and the kernel folds it into its register bias tiles whenever that
+    window type changes.  ``q``'s batch must be a multiple of ``nW`` and
+    ``N`` the window volume.
     """
     assert q.is_cuda and k.is_cuda and v.is_cuda
     assert q.shape == k.shape == v.shape, "Q/K/V shape mismatch"
