@@ -74,7 +74,6 @@ def test_opcheck_reference_ops(dev):
     assert torch.equal(back, x)
 
 
-
 def test_opcheck_attention_and_block_ops(dev):
     ops = torch.ops.crumpet_ops
     B, H, N = 8, 2, 27
