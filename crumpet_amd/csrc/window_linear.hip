@@ -272,6 +272,19 @@ window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln
         const int nch = C >> 2;
         const uint32_t t = t0 + tl;
         const uint32_t row = t < g.tokens ? token_row(t, g) : kPadRow;
+        // LayerNorm parameters requested with the rows (C <= 48), so that
+        // the normalisation does not wait for a second round trip after
+        // them (6% at stage 0; larger C would cost occupancy).
+        constexpr bool kPreLn = kCpl <= 3;
+        f32x4 gmv[kPreLn ? kCpl : 1], btv[kPreLn ? kCpl : 1];
+        if constexpr (kPreLn) {
+#pragma unroll
+            for (int j = 0; j < kCpl; ++j) {
+                const int c = part + 4 * j;
+                gmv[j] = load_param4(ln_w, ln_dtype, 4 * (c < nch ? c : 0), 1.0f);
+                btv[j] = load_param4(ln_b, ln_dtype, 4 * (c < nch ? c : 0), 0.0f);
+            }
+        }
         f32x4 v[kCpl];
         const Tx* xr = x + int64_t(row == kPadRow ? 0 : row) * C;
 #pragma unroll
@@ -305,8 +318,14 @@ window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln
             for (int j = 0; j < kCpl; ++j) {
                 const int c = part + 4 * j;
                 if (c < nch) {
-                    const f32x4 gm = load_param4(ln_w, ln_dtype, 4 * c, 1.0f);
-                    const f32x4 bt = load_param4(ln_b, ln_dtype, 4 * c, 0.0f);
+                    f32x4 gm, bt;
+                    if constexpr (kPreLn) {
+                        gm = gmv[j];
+                        bt = btv[j];
+                    } else {
+                        gm = load_param4(ln_w, ln_dtype, 4 * c, 1.0f);
+                        bt = load_param4(ln_b, ln_dtype, 4 * c, 0.0f);
+                    }
 #pragma unroll
                     for (int e = 0; e < 4; ++e) v[j][e] = __builtin_fmaf((v[j][e] - mean) * rstd, gm[e], bt[e]);
                 }
