@@ -167,21 +167,65 @@ struct TileShape {
     int32_t ostride;  // LDS row stride of the output chunk (elements)
 };
 
+// Weight fragments and bias of a wave's first kPre 16-feature tiles,
+// requested once the tile's rows are staged, before the barrier that
+// publishes them, so that their round trip overlaps the wait at that
+// barrier instead of following it.  Wave w's tiles in the first output chunk
+// are w, w + 4, ...
+template <typename Tc, int kKSteps, int kPre>
+struct WeightPrefetch {
+    typename Mma<Tc>::x4 wf[kPre > 0 ? kPre : 1][kKSteps];
+    f32x4 b4[kPre > 0 ? kPre : 1];
+
+    __device__ __forceinline__ void load(const Tc* __restrict__ w, const Tc* __restrict__ bias,
+                                         const TileShape& ts, int f_begin, int f_end) {
+        typedef typename Mma<Tc>::x4 X4;
+        const int lane = threadIdx.x & 63;
+        const int wave = threadIdx.x >> 6;
+        const int col = lane & 15;
+        const int g = lane >> 4;
+        const int ksteps = ts.C >> 4;
+        const int ft_end = min(f_end, f_begin + ts.fchunk) >> 4;
+#pragma unroll
+        for (int i = 0; i < kPre; ++i) {
+            const int ft = (f_begin >> 4) + wave + 4 * i;
+            if (ft < ft_end) {
+                const Tc* wrow = w + int64_t(16 * ft + col) * ts.C + 4 * g;
+#pragma unroll
+                for (int kk = 0; kk < kKSteps; ++kk)
+                    if (kk < ksteps) wf[i][kk] = *reinterpret_cast<const X4*>(wrow + 16 * kk);
+                b4[i] = bias ? load4(bias + 16 * ft + 4 * g) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+        }
+    }
+};
+
+// Tiles per wave whose weights are requested before the barrier: the first
+// one from C = 96 up (stages 1-3 of Swin UNETR: 9-17% faster); none at
+// C <= 48, where the registers held across the barrier cost more than the
+// overlap gains (stage 0: 7% slower).
+template <int kKSteps>
+constexpr int prefetch_tiles() {
+    return kKSteps > 3 ? 1 : 0;
+}
+
 // GEMM over the staged tile and a coalesced store of the result:
 //   out^T[f][t] = sum_k W[f][k] a[t][k] + bias[f]
 // for this workgroup's features [f_begin, f_end), in chunks of fchunk.
-// Per chunk, wave w takes the 16-feature tiles w, w+4, ...; each tile's
-// weight fragments (from L2) are requested before its MFMAs.  Lane (col, g)
-// ends with features 4g..4g+3 of token 16 s + col, which go to the LDS
-// output chunk.  (Requesting the next tile's fragments during the current
-// one measured slower: the extra registers cost occupancy.)  After a barrier the 256 threads write the chunk as
-// 16-byte vectors, row by row: row r of the tile goes to element offset
-// rows_lds[r] * n_out (rows_lds[r] < 0: not stored).
-template <typename Tc, int kKSteps>
+// Per chunk, wave w takes the 16-feature tiles w, w+4, ...; the first kPre
+// tiles of the first chunk use the fragments in `pre`, later tiles request
+// theirs (from L2) right before their MFMAs.  Lane (col, g) ends with
+// features 4g..4g+3 of token 16 s + col, which go to the LDS output chunk.
+// (Requesting the next tile's fragments during the current one measured
+// slower: the extra registers cost occupancy.)  After a barrier the 256
+// threads write the chunk as 16-byte vectors, row by row: row r of the tile
+// goes to element offset rows_lds[r] * n_out (rows_lds[r] < 0: not stored).
+template <typename Tc, int kKSteps, int kPre>
 __device__ __forceinline__ void gemm_store(const Tc* __restrict__ a_lds, Tc* __restrict__ o_lds,
                                            const int32_t* __restrict__ rows_lds, const Tc* __restrict__ w,
                                            const Tc* __restrict__ bias, Tc* __restrict__ out,
-                                           const TileShape& ts, int f_begin, int f_end) {
+                                           const TileShape& ts, int f_begin, int f_end,
+                                           const WeightPrefetch<Tc, kKSteps, kPre>& pre) {
     typedef typename Mma<Tc>::x4 X4;
     typedef Tc T8 __attribute__((ext_vector_type(16 / sizeof(Tc))));
     const int lane = threadIdx.x & 63;
@@ -191,32 +235,43 @@ __device__ __forceinline__ void gemm_store(const Tc* __restrict__ a_lds, Tc* __r
     const int C = ts.C;
     const int ksteps = C >> 4;
     constexpr int kEpv = 16 / sizeof(Tc);  // elements per 16-byte vector
+
+    // one 16-feature tile: MFMAs over the staged rows, result to the LDS chunk
+    auto tile = [&](int ft, int c0, const X4 (&wf)[kKSteps], const f32x4& b4) {
+        f32x4 acc[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[s] = b4;
+#pragma unroll
+        for (int kk = 0; kk < kKSteps; ++kk) {
+            if (kk < ksteps) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const X4 bf = *reinterpret_cast<const X4*>(&a_lds[(16 * s + col) * ts.astride + 16 * kk + 4 * g]);
+                    acc[s] = Mma<Tc>::step(wf[kk], bf, acc[s]);
+                }
+            }
+        }
+        const int f0 = 16 * ft + 4 * g;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) store4(&o_lds[(16 * s + col) * ts.ostride + (f0 - c0)], acc[s]);
+    };
+
     for (int c0 = f_begin; c0 < f_end; c0 += ts.fchunk) {
         const int c1 = min(f_end, c0 + ts.fchunk);
-        for (int ft = (c0 >> 4) + wave; ft < (c1 >> 4); ft += 4) {
+        int ft = (c0 >> 4) + wave;
+        if (c0 == f_begin) {
+#pragma unroll
+            for (int i = 0; i < kPre; ++i, ft += 4)
+                if (ft < (c1 >> 4)) tile(ft, c0, pre.wf[i], pre.b4[i]);
+        }
+        for (; ft < (c1 >> 4); ft += 4) {
             const Tc* wrow = w + int64_t(16 * ft + col) * C + 4 * g;
             X4 wf[kKSteps];
 #pragma unroll
             for (int kk = 0; kk < kKSteps; ++kk)
                 if (kk < ksteps) wf[kk] = *reinterpret_cast<const X4*>(wrow + 16 * kk);
-            const int f0 = 16 * ft + 4 * g;
-            const f32x4 b4 = bias ? load4(bias + f0) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            f32x4 acc[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) acc[s] = b4;
-#pragma unroll
-            for (int kk = 0; kk < kKSteps; ++kk) {
-                if (kk < ksteps) {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) {
-                        const X4 bf =
-                            *reinterpret_cast<const X4*>(&a_lds[(16 * s + col) * ts.astride + 16 * kk + 4 * g]);
-                        acc[s] = Mma<Tc>::step(wf[kk], bf, acc[s]);
-                    }
-                }
-            }
-#pragma unroll
-            for (int s = 0; s < 4; ++s) store4(&o_lds[(16 * s + col) * ts.ostride + (f0 - c0)], acc[s]);
+            const f32x4 b4 = bias ? load4(bias + 16 * ft + 4 * g) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            tile(ft, c0, wf, b4);
         }
         __syncthreads();
         const int vpr = (c1 - c0) / kEpv;  // vectors per row of this chunk
@@ -337,8 +392,10 @@ window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln
             if (c < nch) store4(&L.a[tl * ts.astride + 4 * c], v[j]);
         }
     }
+    WeightPrefetch<Tc, kCpl, prefetch_tiles<kCpl>()> pre;
+    pre.load(w, bias, ts, f_begin, f_end);
     __syncthreads();
-    gemm_store<Tc, kCpl>(L.a, L.o, L.rows, w, bias, out, ts, f_begin, f_end);
+    gemm_store<Tc, kCpl>(L.a, L.o, L.rows, w, bias, out, ts, f_begin, f_end, pre);
 }
 
 // proj projection + inverse partition + reverse shift + crop.
@@ -369,8 +426,10 @@ window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __r
         if (uint32_t(r) < rows) v = load4(src + int64_t(r) * C + 4 * c);
         store4(&L.a[r * ts.astride + 4 * c], v);
     }
+    WeightPrefetch<Tc, kKSteps, prefetch_tiles<kKSteps>()> pre;
+    pre.load(w, bias, ts, f_begin, f_end);
     __syncthreads();
-    gemm_store<Tc, kKSteps>(L.a, L.o, L.rows, w, bias, y, ts, f_begin, f_end);
+    gemm_store<Tc, kKSteps>(L.a, L.o, L.rows, w, bias, y, ts, f_begin, f_end, pre);
 }
 
 int elem_size(int32_t dtype) {
