@@ -102,6 +102,17 @@ def _compute_dtype(x: torch.Tensor) -> torch.dtype:
     return x.dtype
 
 
+_ESIZE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
+
+
+def _fits_staging_tile(c: int, esize: int) -> bool:
+    """The projections' LDS tile (window_linear.hip plan_tile): 64 staged rows
+    of C channels, an output chunk of at least 16 features (rows padded by
+    16 bytes each) and 64 row indices within 64 KiB."""
+    pad = 16 // esize
+    return 64 * (c + pad) * esize + 64 * (16 + pad) * esize + 64 * 4 <= 64 * 1024
+
+
 def _fused_block_supported(block, x: torch.Tensor) -> bool:
     """Inference-mode blocks whose attention half the fused block kernels
     cover: LayerNorm norm1 over C, Linear qkv / proj, head dimension 16, no
@@ -121,8 +132,7 @@ def _fused_block_supported(block, x: torch.Tensor) -> bool:
         return False
     if attn.attn_drop.p != 0.0 or attn.num_heads * 16 != c:
         return False
-    esize = torch.empty((), dtype=_compute_dtype(x)).element_size()
-    return c % 16 == 0 and c <= 384 and 64 * (c + 16 // esize) * esize <= 64 * 1024
+    return c % 16 == 0 and c <= 384 and _fits_staging_tile(c, _ESIZE[_compute_dtype(x)])
 
 
 def _fused_block_forward(block, x, mask_matrix, swin):

@@ -132,6 +132,24 @@ def test_window_projection_argument_checks_need_no_gpu():
     assert proj(ws=0) == 1 and b"window_size" in lib.crumpet_last_error()
 
 
+def test_fused_block_support_check_matches_the_tile_plan():
+    """monai_patch only routes a block to the fused projections when their
+    LDS tile plan accepts its width: the Python check agrees with the C ABI
+    for every C, in both directions (B = 0 plans the tile and launches
+    nothing)."""
+    from crumpet_amd.monai_patch import _fits_staging_tile
+
+    lib = c_abi()
+    fake = ctypes.c_void_p(256)
+    for dtype, esize in ((0, 4), (1, 2), (2, 2)):
+        for C in range(16, 385, 16):
+            rc_q = lib.crumpet_window_qkv_3d(fake, dtype, fake, dtype, 0, 12, 12, 12, C, 1, None, None, 0,
+                                             ctypes.c_float(1e-5), fake, None, 3 * C, 7, 7, 7, 3, 3, 3, None)
+            rc_p = lib.crumpet_window_proj_3d(fake, fake, dtype, 0, 12, 12, 12, C, fake, None, C,
+                                              7, 7, 7, 3, 3, 3, None)
+            assert (rc_q == 0) == _fits_staging_tile(C, esize) == (rc_p == 0), (dtype, C, rc_q, rc_p)
+
+
 def test_dispatcher_schemas_match_reference():
     import crumpet_amd  # noqa: F401  (loads the binding)
 
