@@ -277,3 +277,25 @@ def test_config3_stage0_shifted_sampled(oracle, dev):
     t = qkv[sample].reshape(len(sample), N, 3, H, Dh).permute(2, 0, 3, 1, 4)
     ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), m[sample % 343], None, scale=0.25)
     _compare(out[torch.from_numpy(sample).to(dev)], ref, dtype, "config3 shifted sample")
+
+
+@pytest.mark.parametrize("N", [1, 2, 15, 16, 17, 63, 64, 65, 128, 129, 224, 225, 352, 353, 511, 512])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_tile_count_boundaries(oracle, dev, N, dtype):
+    """Every tile-count class and its edges (N = 16 t and 16 t + 1, the
+    smallest and largest N of each compiled NT), any N (no window shape
+    implied), with a random fp32 bias and, for odd N, an fp32 mask with
+    boundary flags."""
+    B, H, Dh = 3, 2, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 900 + N)
+    bias = seeded((H, N, N), torch.float32, 901 + N)
+    mask = bnd = None
+    if N % 2:
+        mask = torch.where(seeded((B, N, N), torch.float32, 902 + N) > 0.7, -100.0, 0.0)
+        bnd = torch.tensor([1, 0, 1], dtype=torch.uint8)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None if mask is None else mask.numpy(),
+                           None if bnd is None else bnd.numpy(), scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev),
+                               None if mask is None else mask.to(dev), None if bnd is None else bnd.to(dev),
+                               scale=0.25)
+    _compare(out, ref, dtype, f"N={N} {dtype}")
