@@ -29,6 +29,8 @@ CASES = [  # name, (B, D, H, W, C), ws, ss
     ("s2", (1, 7, 7, 7, 192), (7, 7, 7), (0, 0, 0)),
     ("s3monai", (2, 6, 6, 6, 384), (6, 6, 6), (0, 0, 0)),
     ("noncubic", (1, 7, 9, 5, 32), (7, 3, 5), (2, 1, 0)),
+    ("c16", (2, 9, 9, 9, 16), (7, 7, 7), (3, 3, 3)),        # smallest C, padded
+    ("c224", (1, 7, 8, 7, 224), (7, 7, 7), (3, 3, 3)),      # widest C an fp32 tile takes
 ]
 DTYPES = [  # (x dtype, compute dtype)
     (torch.float32, torch.float16),
@@ -52,8 +54,7 @@ def _compare(got: torch.Tensor, want: np.ndarray, dtype, what: str):
 
 
 def _skip_unsupported(C, cdt):
-    es = torch.empty((), dtype=cdt).element_size()
-    if 64 * (C + 16 // es) * es > 64 * 1024:
+    if not monai_patch._fits_staging_tile(C, torch.empty((), dtype=cdt).element_size()):
         pytest.skip(f"C={C} in {cdt} exceeds the staging tile (unfused path)")
 
 
@@ -208,7 +209,7 @@ def test_fused_forward_part1_matches_eager(dev, dims, dim, heads, shift, autocas
 
     cdt = torch.float16 if autocast else torch.float32
     es = torch.empty((), dtype=cdt).element_size()
-    if 64 * (dim + 16 // es) * es > 64 * 1024:  # C=384 in fp32: the patch keeps the unfused path
+    if not monai_patch._fits_staging_tile(dim, es):  # C=384 in fp32: the patch keeps the unfused path
         with torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
             assert not monai_patch._fused_block_supported(blk, x)
         pytest.skip(f"C={dim} in {cdt} exceeds the staging tile (unfused path)")
