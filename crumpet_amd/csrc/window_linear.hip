@@ -104,6 +104,10 @@ struct WinGeom {
     uint32_t ws_d, ws_h, ws_w;
     uint32_t ss_d, ss_h, ss_w;
     FastDiv f_vol, f_nW, f_nWw, f_nWh, f_wsw, f_wsh;
+    // volume order -> window order (window_proj)
+    uint32_t vtokens;           // B * D0 * H0 * W0
+    uint32_t nWh, nWw, nW, vol;
+    FastDiv f_W0, f_H0, f_D0, f_wsd;
 };
 
 // Row of window-ordered token t in the caller's [B, D0, H0, W0] volume, or
@@ -124,6 +128,25 @@ __device__ __forceinline__ uint32_t token_row(uint32_t t, const WinGeom& g) {
     w -= (w >= g.W) ? g.W : 0u;
     if (d >= g.D0 || h >= g.H0 || w >= g.W0) return kPadRow;
     return ((b * g.D0 + d) * g.H0 + h) * g.W0 + w;
+}
+
+// Window-ordered token of volume token v (< vtokens): the inverse of
+// token_row over the caller's volume.
+__device__ __forceinline__ uint32_t window_token(uint32_t v, const WinGeom& g) {
+    uint32_t t1, w, t2, h, b, d, wd, ld, wh, lh, ww, lw;
+    g.f_W0.divmod(v, t1, w);
+    g.f_H0.divmod(t1, t2, h);
+    g.f_D0.divmod(t2, b, d);
+    // position in the rolled, padded frame: (x - ss) mod padded dim
+    d = (d >= g.ss_d) ? d - g.ss_d : d + g.D - g.ss_d;
+    h = (h >= g.ss_h) ? h - g.ss_h : h + g.H - g.ss_h;
+    w = (w >= g.ss_w) ? w - g.ss_w : w + g.W - g.ss_w;
+    g.f_wsd.divmod(d, wd, ld);
+    g.f_wsh.divmod(h, wh, lh);
+    g.f_wsw.divmod(w, ww, lw);
+    const uint32_t win = (wd * g.nWh + wh) * g.nWw + ww;
+    const uint32_t loc = (ld * g.ws_h + lh) * g.ws_w + lw;
+    return (b * g.nW + win) * g.vol + loc;
 }
 
 // Four consecutive elements of type T as floats (8- or 16-byte load).
@@ -398,7 +421,10 @@ window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln
     gemm_store<Tc, kCpl>(L.a, L.o, L.rows, w, bias, out, ts, f_begin, f_end, pre);
 }
 
-// proj projection + inverse partition + reverse shift + crop.
+// proj projection + inverse partition + reverse shift + crop, in output
+// (volume) order: a workgroup owns 64 consecutive tokens of the caller's
+// volume, gathers their window rows (4 lanes per row, like window_qkv's
+// row loads) and writes 64 consecutive output rows.
 template <typename Tc, int kKSteps>
 __global__ void __launch_bounds__(kThreads)
 window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __restrict__ w,
@@ -410,21 +436,25 @@ window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __r
     const int f_begin = blockIdx.y * ts.fgroup;
     const int f_end = min(ts.n_out, f_begin + ts.fgroup);
     if (threadIdx.x < kTileTokens) {
-        // volume row of each token (the scatter); padding and the tail: none
-        const uint32_t t = t0 + threadIdx.x;
-        const uint32_t row = t < g.tokens ? token_row(t, g) : kPadRow;
-        L.rows[threadIdx.x] = row == kPadRow ? -1 : static_cast<int32_t>(row);
+        const uint32_t v = t0 + threadIdx.x;
+        L.rows[threadIdx.x] = v < g.vtokens ? static_cast<int32_t>(v) : -1;
     }
-    // the tile's 64 window-ordered rows are contiguous: 4-element chunks
-    const int nch = C >> 2;
-    const uint32_t rows = min(uint32_t(kTileTokens), g.tokens - t0);
-    const Tc* src = win + int64_t(t0) * C;
-    for (int i = threadIdx.x; i < kTileTokens * nch; i += kThreads) {
-        const int r = i / nch;
-        const int c = i - r * nch;
-        f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        if (uint32_t(r) < rows) v = load4(src + int64_t(r) * C + 4 * c);
-        store4(&L.a[r * ts.astride + 4 * c], v);
+    {
+        const int lane = threadIdx.x & 63;
+        const int tl = (threadIdx.x >> 6) * 16 + (lane >> 2);
+        const int part = lane & 3;
+        const int nch = C >> 2;
+        const uint32_t v = t0 + tl;
+        const bool in = v < g.vtokens;
+        const Tc* src = win + int64_t(in ? window_token(v, g) : 0) * C;
+#pragma unroll
+        for (int j = 0; j < kKSteps; ++j) {
+            const int c = part + 4 * j;
+            if (c < nch) {
+                const f32x4 x4 = in ? load4(src + 4 * c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                store4(&L.a[tl * ts.astride + 4 * c], x4);
+            }
+        }
     }
     WeightPrefetch<Tc, kKSteps, prefetch_tiles<kKSteps>()> pre;
     pre.load(w, bias, ts, f_begin, f_end);
@@ -470,6 +500,15 @@ int make_geometry(const char* what, int64_t B, int64_t D, int64_t H, int64_t W, 
     g.f_nWh.init(nWh);
     g.f_wsw.init(ws_w);
     g.f_wsh.init(ws_h);
+    g.vtokens = static_cast<uint32_t>(B * D * H * W);
+    g.nWh = nWh;
+    g.nWw = nWw;
+    g.nW = (Dp / ws_d) * nWh * nWw;
+    g.vol = ws_d * ws_h * ws_w;
+    g.f_W0.init(W);
+    g.f_H0.init(H);
+    g.f_D0.init(D);
+    g.f_wsd.init(ws_d);
     return CRUMPET_OK;
 }
 
@@ -627,9 +666,9 @@ extern "C" int crumpet_window_proj_3d(void* y, const void* windows, int32_t dtyp
     TileShape ts;
     size_t lds;
     dim3 grid;
-    st = plan_tile(what, C, n_out, dtype, weight, g.tokens, ts, lds, grid);
+    st = plan_tile(what, C, n_out, dtype, weight, g.vtokens, ts, lds, grid);
     if (st != CRUMPET_OK) return st;
-    if (g.tokens == 0) return CRUMPET_OK;
+    if (g.vtokens == 0) return CRUMPET_OK;
     if (y == nullptr || windows == nullptr)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: null data pointer", what);
     if ((reinterpret_cast<uintptr_t>(y) | reinterpret_cast<uintptr_t>(windows) |
