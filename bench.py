@@ -261,10 +261,23 @@ def bench_blocks(args, dev):
 
             _events_time(step, args.warmup)
             ms = _events_time(step, args.steps)
+            # the same three launches replayed as one HIP graph (no host launch overhead)
+            cap = torch.cuda.Stream()
+            cap.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(cap):
+                step(0)
+            torch.cuda.current_stream().wait_stream(cap)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=cap):
+                step(0)
+            _events_time(lambda i: graph.replay(), args.warmup)
+            ms_graph = _events_time(lambda i: graph.replay(), args.steps)
+            del graph
             tokens = B * dim ** 3
             part_bytes = 2 * tokens * C * x.element_size()
             flops = 4 * N * N * 16 * H * (tokens // N)
-            res[f"{name}_{tag}"] = {"ms": round(ms, 5), "shape": [B, dim, dim, dim, C], "heads": H,
+            res[f"{name}_{tag}"] = {"ms": round(ms, 5), "ms_graph_replay": round(ms_graph, 5),
+                                    "shape": [B, dim, dim, dim, C], "heads": H,
                                     "window": list(ws), "shift": list(ss),
                                     "partition_bytes": part_bytes, "attention_flops": flops,
                                     "effective_GB_s": round(3 * part_bytes / (ms * 1e-3) / 1e9, 1)}
