@@ -39,8 +39,8 @@ def patched():
     crumpet_amd.unpatch_monai_swin_unetr()
 
 
-def _run(module, *args, autocast=False):
-    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16, enabled=autocast):
+def _run(module, *args, autocast=False, dtype=torch.float16):
+    with torch.no_grad(), torch.autocast("cuda", dtype=dtype, enabled=autocast):
         return module(*args)
 
 
@@ -83,6 +83,24 @@ def test_patched_basic_layer_fp16_autocast(patched, dev, block_mode):
     err = (got - want).abs().max().item()
     scale = want.abs().max().item()
     print(f"fp16 autocast: max-abs {err:.2e} (max |x| {scale:.2f})", flush=True)
+    assert err < 1e-2 * scale
+
+
+@pytest.mark.parametrize("dims,dim,heads", [((12, 12, 12), 48, 3), ((6, 6, 6), 384, 24)])
+def test_patched_basic_layer_bf16_autocast(patched, dev, dims, dim, heads, block_mode):
+    """bf16 autocast: eager rounds q k^T to bf16 before the bias and the
+    softmax, the kernel keeps the scores in fp32, so the bound is 1e-2
+    relative to the largest activation, the north-star bf16 tolerance
+    (measured: about 1.6e-3)."""
+    layer = _layer(dim, heads, 4).to(dev).eval()
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn((2, dim) + dims, generator=g).to(dev)
+    want = _run(layer, x, autocast=True, dtype=torch.bfloat16).float()
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(layer, x, autocast=True, dtype=torch.bfloat16).float()
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    print(f"bf16 autocast {dims} C={dim}: max-abs {err:.2e} (max |x| {scale:.2f})", flush=True)
     assert err < 1e-2 * scale
 
 
