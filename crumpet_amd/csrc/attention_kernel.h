@@ -249,13 +249,15 @@ constexpr int waves_per_eu() {
 // Walks the logical window indices [i0, i1) of a workgroup.  In region mode
 // windows are visited grouped by type: logical index -> (type t, outer batch,
 // window choice per axis) in mixed radix.  The start is decoded once; each
-// step is a carry chain of scalar compares (no divisions per window).
+// step is a carry chain of scalar compares (no divisions per window).  In
+// the other modes logical index i is window base + i * stride.
 template <int kMask>
 struct WindowIter {
     int i;
     int t, batch, jd, jh, jw;  // region mode position
     int cd, ch, cw, code;      // choices of the current type, its code
     int batches;               // outer batches (B / nW)
+    int base = 0, stride = 1;  // other modes: window = base + i * stride
 
     __device__ __forceinline__ void load_type(const Params& p) {
         code = p.types.code[t];
@@ -286,7 +288,7 @@ struct WindowIter {
     __device__ __forceinline__ int window(const Params& p, int& type_code) const {
         if constexpr (kMask != kMaskRegion) {
             type_code = 0;
-            return i;
+            return base + i * stride;
         } else {
             const int wd = (code & 4) ? p.nWd - 1 : jd;
             const int wh = (code & 2) ? p.nWh - 1 : jh;
@@ -889,8 +891,14 @@ swin_attention_d16_kernel(const Params p) {
     const int rh = static_cast<int>(chunk / p.groups);
     const int h = rh % p.H;
     const int range = rh / p.H;
-    const int i0 = range * p.win_per_wg;
-    const int i1 = min(p.B, i0 + p.win_per_wg);
+    // Tensor-mask modes take every ranges-th window (range, range + ranges,
+    // ...): a window whose boundary flag is set costs more than one whose
+    // flag is clear, and boundary windows come in runs (the last window
+    // slab of a volume is a run of nWh * nWw), so contiguous ranges would
+    // leave some workgroups with mostly masked windows (17% at config 3).
+    constexpr bool kStrided = kMask == kMaskF16 || kMask == kMaskF32 || kMask == kMaskBF16;
+    const int i0 = kStrided ? 0 : range * p.win_per_wg;
+    const int i1 = kStrided ? (p.B - range + p.ranges - 1) / p.ranges : min(p.B, i0 + p.win_per_wg);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -921,6 +929,10 @@ swin_attention_d16_kernel(const Params p) {
     St st;
     WindowIter<kMask> it;
     it.init(p, i0);
+    if constexpr (kStrided) {
+        it.base = range;
+        it.stride = p.ranges;
+    }
     int code_cur = -1;
     int code_next;
     int b_next = it.window(p, code_next);
