@@ -722,6 +722,10 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
     for (int c0 = 0; c0 < NT; c0 += kChunk) {
         // chunks must not interleave: that would keep two chunks of scores live
         __builtin_amdgcn_sched_barrier(0);
+        // matrix sections run at raised wave priority, the softmax at the
+        // normal one, so that a SIMD's waves tend to alternate between the
+        // two pipes (1-2%)
+        __builtin_amdgcn_s_setprio(1);
         const int cn = (NT - c0 < kChunk) ? NT - c0 : kChunk;
         f32x4 S[kChunk];
 #pragma unroll
@@ -760,6 +764,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
             if constexpr (kUseMask) __builtin_amdgcn_sched_barrier(0);  // keep the mask ring
         }
 
+        __builtin_amdgcn_s_setprio(0);
         // lane-local chunk max: two 3-input maxes per tile on two chains
         float m0 = m_run, m1 = -INFINITY;
 #pragma unroll
@@ -796,6 +801,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
             for (int r = 0; r < 4; ++r) S[u][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[u][r], kLog2e, -mb));
         }
 
+        __builtin_amdgcn_s_setprio(1);
         // O^T += V^T P^T; the row sums ride on the matrix pipe as ones^T P^T
         if constexpr (sizeof(T) == 2) {
             typedef typename Frag<T>::x8 X8;
@@ -848,6 +854,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
             }
         }
     }
+    __builtin_amdgcn_s_setprio(0);
     float l;
     if constexpr (sizeof(T) == 2) {
         l = lacc[0];  // every row of ones^T P^T holds the sum for query col
