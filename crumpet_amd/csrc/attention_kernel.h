@@ -12,7 +12,8 @@
 //   The relative-position bias is the same for every window, so it is kept in
 //   registers instead of being re-read per window: a workgroup of 4 waves
 //   owns one head h and a group of 4 consecutive 16-query strips, and walks a
-//   contiguous range of windows.  Each wave builds the fp32 bias tiles of its
+//   range of windows (contiguous; every ranges-th window with a mask tensor,
+//   whose boundary windows cost more and come in runs).  Each wave builds the fp32 bias tiles of its
 //   strip (NT tiles of 16 keys x 16 queries, 4 values per lane each) once,
 //   straight from the caller's bias tensor (any float dtype and strides),
 //   and uses them as the accumulator input of every window's S^T = K Q^T
