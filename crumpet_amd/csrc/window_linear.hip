@@ -9,7 +9,8 @@
 // puts at t: d = (wd*ws_d + ld + ss_d) mod D, likewise for h and w, on the
 // volume zero-padded to the window grid (D, H, W multiples of ws).  Tokens
 // whose src lies in the padding read zeros (the padding is applied after
-// the LayerNorm) and are not stored by window_proj (the crop).
+// the LayerNorm); window_proj produces only the tokens inside the caller's
+// volume (the crop).
 //
 // This is the eager chain of MONAI's SwinTransformerBlock.forward_part1 and
 // WindowAttention (norm1, F.pad, torch.roll, window_partition, qkv Linear;
@@ -21,12 +22,15 @@
 // output once and writes the block output once.
 //
 // Both kernels are one GEMM with M = output features, N = tokens, K = C on
-// the matrix cores: a workgroup of 4 waves owns 64 consecutive window-ordered
-// tokens whose (normalised) rows it stages in LDS as the B operand; each wave
-// walks a quarter of the 16-feature output tiles, reading its weight
-// fragments (the A operand) straight from the L2-resident weight matrix.
-// The MFMA result layout gives each lane 4 consecutive output features of
-// one token, i.e. one 8-byte (fp16/bf16) or 16-byte (fp32) store.
+// the matrix cores, in output order: a workgroup of 4 waves owns 64
+// consecutive output tokens (window-ordered for window_qkv, volume-ordered
+// for window_proj, so padding is never loaded or computed there), gathers
+// their input rows (4 lanes per row) and stages them in LDS as the B
+// operand; each wave walks a quarter of the 16-feature output tiles,
+// reading its weight fragments (the A operand) straight from the
+// L2-resident weight matrix.  The MFMA result layout gives each lane 4
+// consecutive output features of one token; they go to an LDS output chunk
+// that the workgroup writes back as consecutive 16-byte vectors.
 //
 // Numerics: LayerNorm in fp32 (two passes: mean, then the mean of squared
 // deviations; biased variance, as torch), the normalised value rounded once
