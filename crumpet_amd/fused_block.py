@@ -13,8 +13,9 @@ Here it is three gfx950 kernels:
   projection in one pass over the block input (``crumpet_window_qkv_3d``);
 * the fused window attention (``crumpet_fused_swin_attention[_shifted]``),
   reading q, k, v as strided views of the qkv buffer;
-* ``window_proj_3d``: the proj projection with the reverse partition, shift
-  and crop folded into its stores (``crumpet_window_proj_3d``).
+* ``window_proj_3d``: the proj projection in output (volume) order, the
+  reverse partition, shift and crop folded into its row gathers
+  (``crumpet_window_proj_3d``).
 
 The layout changes never touch HBM as separate passes.  Numerics follow the
 eager chain under autocast: LayerNorm in fp32, its output rounded once to
