@@ -25,7 +25,7 @@
 // the matrix cores, in output order: a workgroup of 4 waves owns 64
 // consecutive output tokens (window-ordered for window_qkv, volume-ordered
 // for window_proj, so padding is never loaded or computed there), gathers
-// their input rows (4 lanes per row) and stages them in LDS as the B
+// their input rows and stages them in LDS as the B
 // operand; each wave walks a quarter of the 16-feature output tiles,
 // reading its weight fragments (the A operand) straight from the
 // L2-resident weight matrix.  The MFMA result layout gives each lane 4
@@ -427,8 +427,8 @@ window_qkv_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln
 
 // proj projection + inverse partition + reverse shift + crop, in output
 // (volume) order: a workgroup owns 64 consecutive tokens of the caller's
-// volume, gathers their window rows (4 lanes per row, like window_qkv's
-// row loads) and writes 64 consecutive output rows.
+// volume, gathers their window rows as 16-byte vectors (adjacent lanes on
+// adjacent parts of a row) and writes 64 consecutive output rows.
 template <typename Tc, int kKSteps>
 __global__ void __launch_bounds__(kThreads)
 window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __restrict__ w,
@@ -444,20 +444,34 @@ window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __r
         L.rows[threadIdx.x] = v < g.vtokens ? static_cast<int32_t>(v) : -1;
     }
     {
-        const int lane = threadIdx.x & 63;
-        const int tl = (threadIdx.x >> 6) * 16 + (lane >> 2);
-        const int part = lane & 3;
-        const int nch = C >> 2;
-        const uint32_t v = t0 + tl;
-        const bool in = v < g.vtokens;
-        const Tc* src = win + int64_t(in ? window_token(v, g) : 0) * C;
+        // Rows are copied as 16-byte vectors, vector i of the tile being
+        // (token i / vpt, part i mod vpt): adjacent lanes read adjacent parts
+        // of a row, and the rows of tokens adjacent along W within a window
+        // are adjacent in the window buffer, so a wave reads whole runs.  All
+        // of a lane's loads are issued before its LDS stores.
+        typedef uint32_t V16 __attribute__((ext_vector_type(4)));
+        constexpr int kEpv16 = 16 / sizeof(Tc);
+        constexpr int kIters = (kTileTokens * (16 * kKSteps / kEpv16) + kThreads - 1) / kThreads;
+        constexpr int kBatch = kIters < 3 ? kIters : 3;  // loads in flight per lane
+        const int vpt = C / kEpv16;
+        const int total = kTileTokens * vpt;
+        for (int i0 = threadIdx.x; i0 < total; i0 += kBatch * kThreads) {
+            V16 xv[kBatch];
+            int dst[kBatch];
 #pragma unroll
-        for (int j = 0; j < kKSteps; ++j) {
-            const int c = part + 4 * j;
-            if (c < nch) {
-                const f32x4 x4 = in ? load4(src + 4 * c) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-                store4(&L.a[tl * ts.astride + 4 * c], x4);
+            for (int u = 0; u < kBatch; ++u) {
+                const int i = i0 + u * kThreads;
+                const int tl = i / vpt;
+                const int part = i - tl * vpt;
+                const uint32_t v = t0 + tl;
+                xv[u] = V16{0u, 0u, 0u, 0u};
+                dst[u] = i < total ? tl * ts.astride + part * kEpv16 : -1;
+                if (i < total && v < g.vtokens)
+                    xv[u] = *reinterpret_cast<const V16*>(win + int64_t(window_token(v, g)) * C + part * kEpv16);
             }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (dst[u] >= 0) *reinterpret_cast<V16*>(&L.a[dst[u]]) = xv[u];
         }
     }
     WeightPrefetch<Tc, kKSteps, prefetch_tiles<kKSteps>()> pre;
