@@ -49,12 +49,20 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     if (B < 0 || Hh < 0 || N < 0 || Dh <= 0)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: negative size", what);
     if (B == 0 || Hh == 0 || N == 0) return CRUMPET_OK;
-    if (Dh != 16)
-        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: head_dim %lld is not supported (16)", what,
-                    (long long)Dh);
-    if (N > 512)
-        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: N = %lld exceeds 512 tokens per window", what,
-                    (long long)N);
+    // head dim 16 with N <= 512 (every Swin UNETR stage) runs the tuned
+    // kernel; other head dims and larger windows the general one
+    if (Dh != 16 && Dh != 32 && Dh != 64 && Dh != 128)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: head_dim %lld is not supported (16, 32, 64 or 128)",
+                    what, (long long)Dh);
+    const bool wide = Dh != 16 || N > 512;
+    if (wide && N > 0x3fffffffLL)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: N = %lld is too large", what, (long long)N);
+    if (wide && region != nullptr && N > attn::kWideMaxRegionN)
+        return fail(CRUMPET_ERR_UNSUPPORTED,
+                    "%s: shifted windows of %lld tokens exceed %d", what, (long long)N,
+                    attn::kWideMaxRegionN);
+    if (wide && B * Hh * ((N + attn::kWideQueries - 1) / attn::kWideQueries) >= 0x7fffff00LL)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: too many (window, head, query block) triples", what);
     if (B * Hh > 0x7fffffffLL || B > 0x3fffffffLL)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: too many (window, head) pairs", what);
     if (!out || !q || !k || !v || !bias || !out_strides || !q_strides || !k_strides ||
@@ -143,7 +151,6 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         }
     }
 
-    const int NT = attn::select_tiles(N);
     p.q = q;
     p.k = k;
     p.v = v;
@@ -165,6 +172,18 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.B = static_cast<int32_t>(B);
     p.H = static_cast<int32_t>(Hh);
     p.N = static_cast<int32_t>(N);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const int kmask = region != nullptr                  ? attn::kMaskRegion
+                      : mask == nullptr                  ? attn::kNoMask
+                      : mask_dtype == CRUMPET_DTYPE_F32  ? attn::kMaskF32
+                      : mask_dtype == CRUMPET_DTYPE_BF16 ? attn::kMaskBF16
+                                                         : attn::kMaskF16;
+    if (wide) {
+        attn::launch_wide(p, static_cast<int>(Dh), kmask, dtype, mask_dtype, s);
+        return check_launch(what);
+    }
+
+    const int NT = attn::select_tiles(N);
     p.strips = static_cast<int32_t>((N + 15) / 16);
     p.groups = (p.strips + attn::kWaves - 1) / attn::kWaves;
     const int64_t units = Hh * p.groups;
@@ -193,12 +212,6 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     }
     p.vec_io = vec ? 1 : 0;
 
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const int kmask = region != nullptr                  ? attn::kMaskRegion
-                      : mask == nullptr                  ? attn::kNoMask
-                      : mask_dtype == CRUMPET_DTYPE_F32  ? attn::kMaskF32
-                      : mask_dtype == CRUMPET_DTYPE_BF16 ? attn::kMaskBF16
-                                                         : attn::kMaskF16;
     if (dtype == CRUMPET_DTYPE_F16)
         attn::launch_f16(p, NT, kmask, s);
     else if (dtype == CRUMPET_DTYPE_BF16)

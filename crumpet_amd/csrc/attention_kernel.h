@@ -130,6 +130,14 @@ void launch_f16(const Params& p, int NT, int kmask, hipStream_t s);
 void launch_bf16(const Params& p, int NT, int kmask, hipStream_t s);
 void launch_f32(const Params& p, int NT, int kmask, hipStream_t s);
 
+// General kernel (attention_wide.hip): head dims 16, 32, 64 and 128, any N
+// (shifted-window regions up to kWideMaxRegionN tokens).  The caller has
+// checked the head dim, the region size and that B * H * ceil(N / 64) fits
+// in 31 bits.
+constexpr int kWideMaxRegionN = 2048;
+constexpr int kWideQueries = 64;  // queries per workgroup of the general kernel
+void launch_wide(const Params& p, int Dh, int kmask, int32_t dtype, int32_t mask_dtype, hipStream_t s);
+
 // Tile counts the kernel is compiled for; a call runs with the smallest one
 // that covers ceil(N / 16).
 constexpr int kTileCounts[] = {1, 2, 4, 8, 14, 22, 32};

@@ -1,0 +1,308 @@
+// General fused window attention for the shapes the head-dim-16 kernel does
+// not cover: head dims 32, 64 and 128, and windows of more than 512 tokens
+// (any head dim of 16..128 that is a power of two, any N).  Same contract,
+// same numerics and the same three mask modes as swin_attention_d16_kernel
+// (attention_kernel.h):
+//
+//   S = (q * scale) k^T + bias[h] + mask,  out = softmax_rows(S) v
+//
+// with q scaled in fp32 and rounded back to the input type, S and the
+// softmax in fp32, P rounded to the input type for the P v product, the row
+// sums accumulated from the unrounded fp32 P, and one division at the end:
+// the steps of torch-ext/crumpet/fused_attention.py:82-146 in the reference.
+//
+// Decomposition: a workgroup of 4 waves owns one (window, head) and 64
+// queries (a 16-query strip per wave); it walks the keys in chunks of 64,
+// staging K (row-major) and V^T in LDS, and keeps the strip's Q fragments,
+// the online-softmax state and the O^T accumulators in registers.  Per
+// 16-key tile: S^T = K Q^T on the matrix cores over D/16 16-dim steps,
+// starting from the bias (+ mask) tile; per chunk one online-softmax update;
+// then O^T += V^T P^T with P straight from the score registers (the score
+// tile's layout is the B-operand layout).  Bias and mask are read as floats
+// of their own dtype with their own strides.  Nothing is allocated.
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+
+#include "attention_kernel.h"
+#include "crumpet_common.h"
+#include "crumpet_hip.h"
+
+namespace crumpet {
+namespace attn {
+namespace {
+
+constexpr int kWideThreads = 256;
+constexpr int kWideWaves = 4;
+constexpr int kKeyChunk = 64;  // keys staged per LDS chunk
+constexpr float kWideLog2e = 1.4426950408889634f;
+
+typedef float f32x4w __attribute__((ext_vector_type(4)));
+typedef short i16x4w __attribute__((ext_vector_type(4)));
+
+// One 16x16x16 step D += A B; fp32 contracts k = 4g + j in step j for A and
+// B alike, so each product is taken once.
+template <typename T>
+struct WideMma;
+
+template <>
+struct WideMma<_Float16> {
+    typedef _Float16 x4 __attribute__((ext_vector_type(4)));
+    static __device__ __forceinline__ f32x4w step(x4 a, x4 b, f32x4w c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct WideMma<__bf16> {
+    typedef __bf16 x4 __attribute__((ext_vector_type(4)));
+    static __device__ __forceinline__ f32x4w step(x4 a, x4 b, f32x4w c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4w, a),
+                                                         __builtin_bit_cast(i16x4w, b), c, 0, 0, 0);
+    }
+};
+
+template <>
+struct WideMma<float> {
+    typedef f32x4w x4;
+    static __device__ __forceinline__ f32x4w step(x4 a, x4 b, f32x4w c) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+        return c;
+    }
+};
+
+// Element i of a float tensor of dtype dt (uniform branch).
+__device__ __forceinline__ float load_as_float(const void* base, int64_t i, int32_t dt) {
+    if (dt == CRUMPET_DTYPE_F32) return static_cast<const float*>(base)[i];
+    if (dt == CRUMPET_DTYPE_F16) return static_cast<float>(static_cast<const _Float16*>(base)[i]);
+    return static_cast<float>(static_cast<const __bf16*>(base)[i]);
+}
+
+// kMode: 0 no mask, 1 mask tensor (mask[b mod mask_batch], skipped where a
+// boundary flag is 0), 2 shifted-window regions of the [D, H, W] volume.
+template <typename T, int D, int kMode>
+__global__ void __launch_bounds__(kWideThreads)
+swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks, uint32_t chunks,
+                           uint32_t launched) {
+    typedef WideMma<T> M;
+    typedef typename M::x4 X4;
+    constexpr int kDC = D / 16;                                 // 16-dim steps
+    constexpr int kPad = 16 / static_cast<int>(sizeof(T));      // 16 bytes per LDS row
+    constexpr int kKStride = D + kPad;                          // K row stride (elements)
+    constexpr int kVStride = kKeyChunk + kPad;                  // V^T row stride (elements)
+    __shared__ __attribute__((aligned(16))) T k_lds[kKeyChunk * kKStride];
+    __shared__ __attribute__((aligned(16))) T vt_lds[D * kVStride];
+    __shared__ uint8_t cls_lds[kMode == 2 ? kWideMaxRegionN : 4];
+
+    uint32_t chunk;
+    if (!xcd_chunk(blockIdx.x, launched, chunks, chunk)) return;
+    // chunk = (b * H + h) * qblocks + qb: the query blocks of one
+    // (window, head) are consecutive, hence on one XCD, and share its L2.
+    const int qb = static_cast<int>(chunk % qblocks);
+    const uint32_t bh = chunk / qblocks;
+    const int h = static_cast<int>(bh % static_cast<uint32_t>(p.H));
+    const int b = static_cast<int>(bh / static_cast<uint32_t>(p.H));
+    const int N = p.N;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int g = lane >> 4;
+    const int qi = qb * kWideQueries + wave * 16 + col;
+    const int qr = qi < N ? qi : N - 1;  // padded query rows are computed, never stored
+
+    // region mode: shift-region class of every token (one bit per axis, set
+    // at or past ws - ss) and the split bits of this window (axes along which
+    // it is the last window of a shifted axis); tokens of different regions
+    // along a split axis see -100
+    int split = 0;
+    if constexpr (kMode == 2) {
+        for (int j = threadIdx.x; j < N; j += kWideThreads) {
+            const int lw = j % p.ws[2];
+            const int t = j / p.ws[2];
+            const int lh = t % p.ws[1];
+            const int ld = t / p.ws[1];
+            cls_lds[j] = static_cast<uint8_t>(((ld >= p.ws[0] - p.ss[0]) ? 4 : 0) |
+                                              ((lh >= p.ws[1] - p.ss[1]) ? 2 : 0) |
+                                              ((lw >= p.ws[2] - p.ss[2]) ? 1 : 0));
+        }
+        const int wi = b % p.nW;
+        const int ww = wi % p.nWw;
+        const int wt = wi / p.nWw;
+        const int wh = wt % p.nWh;
+        const int wd = wt / p.nWh;
+        split = ((wd == p.nWd - 1 && p.ss[0] > 0) ? 4 : 0) | ((wh == p.nWh - 1 && p.ss[1] > 0) ? 2 : 0) |
+                ((ww == p.nWw - 1 && p.ss[2] > 0) ? 1 : 0);
+    }
+    bool use_mask = false;
+    const void* mask_row = nullptr;
+    if constexpr (kMode == 1) {
+        use_mask = p.boundary == nullptr || p.boundary[b] != 0;
+        const int msz = mask_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
+        mask_row = static_cast<const char*>(p.mask) +
+                   (int64_t(b % p.mask_batch) * p.ms[0] + int64_t(qr) * p.ms[1]) * msz;
+    }
+    const int bsz = p.bias_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
+    const void* bias_row =
+        static_cast<const char*>(p.bias) + (int64_t(h) * p.bsd[0] + int64_t(qr) * p.bsd[1]) * bsz;
+
+    // B operand of S^T = K Q^T: Q[qr][16 dc + 4 g + r], scaled in fp32 and
+    // rounded back to T
+    const T* qrow = static_cast<const T*>(p.q) + int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1] +
+                    int64_t(qr) * p.qs[2];
+    X4 qf[kDC];
+#pragma unroll
+    for (int dc = 0; dc < kDC; ++dc)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            qf[dc][r] = static_cast<T>(static_cast<float>(qrow[int64_t(16 * dc + 4 * g + r) * p.qs[3]]) * p.scale);
+
+    const T* kbase = static_cast<const T*>(p.k) + int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1];
+    const T* vbase = static_cast<const T*>(p.v) + int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1];
+
+    f32x4w o[kDC];  // O^T: o[dd][r] = O[query col][16 dd + 4 g + r]
+#pragma unroll
+    for (int dd = 0; dd < kDC; ++dd) o[dd] = f32x4w{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -INFINITY;
+    float l_part = 0.0f;  // this lane's share of the row sum (its keys 4g..4g+3 of each tile)
+    int my_cls = 0;  // region class of this lane's query (region mode)
+
+    for (int kc0 = 0; kc0 < N; kc0 += kKeyChunk) {
+        __syncthreads();  // the previous chunk's LDS reads are done (first: the class table is written)
+        if constexpr (kMode == 2)
+            if (kc0 == 0) my_cls = cls_lds[qr];
+        // stage K rows and V^T of keys kc0..kc0+63 (zeros past N)
+        for (int e = threadIdx.x; e < kKeyChunk * (D / 4); e += kWideThreads) {
+            const int key = e / (D / 4);
+            const int d0 = (e % (D / 4)) * 4;
+            const int kk = kc0 + key;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                T kv = static_cast<T>(0.0f), vv = static_cast<T>(0.0f);
+                if (kk < N) {
+                    kv = kbase[int64_t(kk) * p.ks[2] + int64_t(d0 + r) * p.ks[3]];
+                    vv = vbase[int64_t(kk) * p.vs[2] + int64_t(d0 + r) * p.vs[3]];
+                }
+                k_lds[key * kKStride + d0 + r] = kv;
+                vt_lds[(d0 + r) * kVStride + key] = vv;
+            }
+        }
+        __syncthreads();
+
+        // scores of the chunk's 4 key tiles: lane (col, g) holds
+        // S[query col][key kc0 + 16 t + 4 g + r]
+        f32x4w S[kKeyChunk / 16];
+#pragma unroll
+        for (int t = 0; t < kKeyChunk / 16; ++t) {
+            f32x4w c;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int kk = kc0 + 16 * t + 4 * g + r;
+                float bv = -INFINITY;
+                if (kk < N) {
+                    bv = load_as_float(bias_row, kk, p.bias_dtype);
+                    if constexpr (kMode == 1)
+                        if (use_mask) bv += load_as_float(mask_row, kk, mask_dtype);
+                    if constexpr (kMode == 2)
+                        if ((my_cls ^ cls_lds[kk]) & split) bv += -100.0f;
+                }
+                c[r] = bv;
+            }
+#pragma unroll
+            for (int dc = 0; dc < kDC; ++dc) {
+                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[(16 * t + col) * kKStride + 16 * dc + 4 * g]);
+                c = M::step(kf, qf[dc], c);
+            }
+            S[t] = c;
+        }
+
+        // online softmax over the chunk: row max across the 4 lane groups
+        float cm = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < kKeyChunk / 16; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cm = fmaxf(cm, S[t][r]);
+        cm = fmaxf(cm, __shfl_xor(cm, 16));
+        cm = fmaxf(cm, __shfl_xor(cm, 32));
+        const float m_new = fmaxf(m_run, cm);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;  // rows with no finite score yet
+        const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * kWideLog2e);
+        l_part *= alpha;
+#pragma unroll
+        for (int dd = 0; dd < kDC; ++dd) o[dd] *= alpha;
+        m_run = m_new;
+        const float mb = m_use * kWideLog2e;
+
+#pragma unroll
+        for (int t = 0; t < kKeyChunk / 16; ++t) {
+            X4 pb;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(S[t][r], kWideLog2e, -mb));
+                l_part += pv;
+                pb[r] = static_cast<T>(pv);
+            }
+            // O^T += V^T P^T: A = V^T[16 dd + col][keys 16 t + 4 g ..], B = P^T
+#pragma unroll
+            for (int dd = 0; dd < kDC; ++dd) {
+                const X4 vf = *reinterpret_cast<const X4*>(&vt_lds[(16 * dd + col) * kVStride + 16 * t + 4 * g]);
+                o[dd] = M::step(vf, pb, o[dd]);
+            }
+        }
+    }
+
+    float l = l_part;
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (qi < N) {
+        T* orow = static_cast<T*>(p.out) + int64_t(b) * p.os[0] + int64_t(h) * p.os[1] + int64_t(qi) * p.os[2];
+#pragma unroll
+        for (int dd = 0; dd < kDC; ++dd)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) orow[int64_t(16 * dd + 4 * g + r) * p.os[3]] = static_cast<T>(o[dd][r] / l);
+    }
+}
+
+template <typename T, int D>
+void launch_d(const Params& p, int mode, int32_t mask_dtype, uint32_t qblocks, uint32_t chunks,
+              uint32_t launched, hipStream_t s) {
+    const dim3 grid(launched), block(kWideThreads);
+    if (mode == 0)
+        hipLaunchKernelGGL((swin_attention_wide_kernel<T, D, 0>), grid, block, 0, s, p, mask_dtype, qblocks,
+                           chunks, launched);
+    else if (mode == 1)
+        hipLaunchKernelGGL((swin_attention_wide_kernel<T, D, 1>), grid, block, 0, s, p, mask_dtype, qblocks,
+                           chunks, launched);
+    else
+        hipLaunchKernelGGL((swin_attention_wide_kernel<T, D, 2>), grid, block, 0, s, p, mask_dtype, qblocks,
+                           chunks, launched);
+}
+
+template <typename T>
+void launch_t(const Params& p, int Dh, int mode, int32_t mask_dtype, uint32_t qblocks, uint32_t chunks,
+              uint32_t launched, hipStream_t s) {
+    switch (Dh) {
+        case 16: launch_d<T, 16>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
+        case 32: launch_d<T, 32>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
+        case 64: launch_d<T, 64>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
+        default: launch_d<T, 128>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
+    }
+}
+
+}  // namespace
+
+void launch_wide(const Params& p, int Dh, int kmask, int32_t dtype, int32_t mask_dtype, hipStream_t s) {
+    const uint32_t qblocks = static_cast<uint32_t>((p.N + kWideQueries - 1) / kWideQueries);
+    const uint32_t chunks = static_cast<uint32_t>(uint64_t(p.B) * uint64_t(p.H) * qblocks);
+    const uint32_t launched = xcd_launch_count(chunks);
+    const int mode = kmask == kMaskRegion ? 2 : kmask == kNoMask ? 0 : 1;
+    if (dtype == CRUMPET_DTYPE_F16)
+        launch_t<_Float16>(p, Dh, mode, mask_dtype, qblocks, chunks, launched, s);
+    else if (dtype == CRUMPET_DTYPE_BF16)
+        launch_t<__bf16>(p, Dh, mode, mask_dtype, qblocks, chunks, launched, s);
+    else
+        launch_t<float>(p, Dh, mode, mask_dtype, qblocks, chunks, launched, s);
+}
+
+}  // namespace attn
+}  // namespace crumpet

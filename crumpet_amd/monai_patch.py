@@ -18,8 +18,10 @@ the originals; True / False likewise) replace
   -> @ v`` chain becomes one gfx950 kernel call (reference :117-198).  It
   falls back to the original in training mode, with attention dropout,
   when ``CRUMPET_DISABLE_FUSED_ATTN=1``, or for a head dimension other
-  than 16 (the kernel's only head dimension; every Swin UNETR stage has
-  16).
+  than 16, 32, 64 or 128 (the kernels' head dimensions; every stage of the
+  feature-size-48 Swin UNETR has 16, feature size 96 gives 32).  The
+  reference takes the fused path for any head dimension from 16 up
+  (reference :144-149), which its Triton kernel compiles for powers of two.
 
 Differences from the reference's patched attention, none of which changes
 the math:
@@ -103,6 +105,8 @@ def _compute_dtype(x: torch.Tensor) -> torch.dtype:
 
 
 _ESIZE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
+# head dimensions of the fused attention kernels
+_HEAD_DIMS = (16, 32, 64, 128)
 
 
 def _fits_staging_tile(c: int, esize: int) -> bool:
@@ -115,8 +119,9 @@ def _fits_staging_tile(c: int, esize: int) -> bool:
 
 def _fused_block_supported(block, x: torch.Tensor) -> bool:
     """Inference-mode blocks whose attention half the fused block kernels
-    cover: LayerNorm norm1 over C, Linear qkv / proj, head dimension 16, no
-    attention dropout, C a multiple of 16 that fits the staging tile."""
+    cover: LayerNorm norm1 over C, Linear qkv / proj, a head dimension the
+    attention kernels take, no attention dropout, C a multiple of 16 that
+    fits the staging tile."""
     attn = block.attn
     c = x.shape[-1]
     if block.training or not (_fused_attn_enabled() and _fused_block_enabled()):
@@ -130,7 +135,7 @@ def _fused_block_supported(block, x: torch.Tensor) -> bool:
         return False
     if attn.qkv.out_features != 3 * c or attn.proj.in_features != c or attn.proj.out_features != c:
         return False
-    if attn.attn_drop.p != 0.0 or attn.num_heads * 16 != c:
+    if attn.attn_drop.p != 0.0 or c % attn.num_heads != 0 or c // attn.num_heads not in _HEAD_DIMS:
         return False
     return c % 16 == 0 and c <= 384 and _fits_staging_tile(c, _ESIZE[_compute_dtype(x)])
 
@@ -202,7 +207,7 @@ def _patched_window_attention_forward(original):
         b, n, c = x.shape
         heads = self.num_heads
         hd = c // heads
-        if hd != 16 or hd * heads != c:
+        if hd not in _HEAD_DIMS or hd * heads != c:
             return original(self, x, mask)
 
         qkv = self.qkv(x)  # [b, n, 3c]; channel = s*c + h*hd + d

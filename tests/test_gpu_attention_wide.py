@@ -1,0 +1,186 @@
+"""Parity of the general attention kernel (head dims 32, 64, 128; windows
+of more than 512 tokens) with the fp32 oracle formula
+softmax(q*scale @ k^T + bias + [boundary]*mask) @ v (oracle/oracle.py).
+
+The reference's Triton kernel takes any power-of-two head dim from 16 up
+and any N (torch-ext/crumpet/fused_attention.py:149-226); its MONAI patch
+routes every head dim >= 16 to it (torch-ext/crumpet/monai_patch.py:144-149).
+Same tolerances as the head-dim-16 kernel: 2e-3 fp16, 1e-2 bf16, 1e-4 fp32
+max-abs vs fp32 on the same low-precision inputs.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import crumpet_amd
+from crumpet_amd.fused_attention import fused_swin_attention, fused_swin_attention_shifted
+from crumpet_amd import swin_unetr_compat as sw
+from helpers import TOL, bias_from_table, boundary_flags, seeded, trunc_normal_table
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float16, torch.bfloat16, torch.float32]
+
+
+def _inputs(B, H, N, D, dtype, seed):
+    return tuple(seeded((B, H, N, D), dtype, seed + i) for i in range(3))
+
+
+def _f32(t):
+    return t.float().numpy()
+
+
+def _compare(out, ref, dtype, what):
+    got = out.float().cpu().numpy()
+    err = np.abs(got - ref).max()
+    print(f"{what}: max-abs {err:.3e} (tol {TOL[dtype]})", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= TOL[dtype], f"{what}: max-abs {err} > {TOL[dtype]}"
+
+
+@pytest.mark.parametrize("Dh", [32, 64, 128])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_head_dims_shifted_mask_with_boundary(oracle, dev, Dh, dtype):
+    """Per-window shifted masks of a 14^3 volume tiled over 2 samples, with
+    boundary flags, N = 343, fp32 bias from a trunc-normal table."""
+    D, ws, ss = 14, (7, 7, 7), (3, 3, 3)
+    B, H, N = 16, 2, 343
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3000 + Dh)
+    bias = bias_from_table(trunc_normal_table(2197, H, 3010 + Dh), ws)
+    m8 = torch.from_numpy(oracle.attn_mask(D, D, D, ws, ss, "float32")).to(dtype)
+    mask = m8.repeat(2, 1, 1)
+    bnd = boundary_flags(D, D, D, ws, ss, outer=2)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), bnd.numpy(), scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), bnd.to(dev),
+                               scale=0.25)
+    assert out.dtype == dtype and out.shape == q.shape
+    _compare(out, ref, dtype, f"Dh={Dh} {dtype} tensor mask")
+
+
+@pytest.mark.parametrize("Dh", [32, 64, 128])
+@pytest.mark.parametrize("N", [1, 27, 64, 65, 216])
+def test_head_dims_no_mask_default_scale(oracle, dev, Dh, N):
+    """No mask, the default scale Dh^-0.5, key counts around the 64-key
+    chunk and 64-query block edges."""
+    dtype = torch.float16
+    B, H = 3, 3
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3100 + N + Dh)
+    bias = seeded((H, N, N), torch.float32, 3150 + N) * 0.1
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=None)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), None)
+    _compare(out, ref, dtype, f"Dh={Dh} N={N} no mask")
+
+
+@pytest.mark.parametrize("mdt", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+def test_head_dim_32_broadcast_mask_dtypes_and_bias_dtype(oracle, dev, mdt):
+    """A [1, N, N] mask of each dtype broadcast over the batch, a bf16 bias
+    with fp16 q/k/v."""
+    dtype = torch.float16
+    B, H, N, Dh = 4, 2, 125, 32
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3200)
+    bias = (seeded((H, N, N), torch.float32, 3210) * 0.2).to(torch.bfloat16)
+    mask = torch.where(seeded((1, N, N), torch.float32, 3220) > 0.6, -100.0, 0.0).to(mdt)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), None, scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), scale=0.25)
+    _compare(out, ref, dtype, f"broadcast {mdt} mask")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_head_dim_32_strided_qkv_views_and_strided_out(oracle, dev, dtype):
+    """q/k/v as views of a [b, n, 3*H*Dh] qkv tensor (MONAI's layout) and
+    out written into a [b, n, H*Dh] buffer through a permuted view."""
+    b, n, H, Dh = 6, 343, 3, 32
+    qkv = seeded((b, n, 3 * H * Dh), dtype, 3300)
+    bias = bias_from_table(trunc_normal_table(2197, H, 3301), (7, 7, 7)).to(dtype)
+    t = qkv.reshape(b, n, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), None, None, scale=0.25)
+    td = qkv.to(dev).reshape(b, n, 3, H, Dh).permute(2, 0, 3, 1, 4)
+    out_bnc = torch.empty((b, n, H * Dh), dtype=dtype, device=dev)
+    out = out_bnc.view(b, n, H, Dh).permute(0, 2, 1, 3)
+    fused_swin_attention(td[0], td[1], td[2], bias.to(dev), None, scale=0.25, out=out)
+    _compare(out, ref, dtype, f"strided {dtype}")
+
+
+@pytest.mark.parametrize("Dh", [16, 32])
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_shifted_regions_general_kernel(oracle, dev, Dh, dtype):
+    """Region mode of the general kernel: head dim 32 at window 7 (N = 343),
+    and head dim 16 at window 9 (N = 729 > 512), against the
+    compute_attn_mask_3d mask tiled over the outer batch."""
+    vol, ws, ss = ((14, 14, 14), (7, 7, 7), (3, 3, 3)) if Dh == 32 else ((18, 18, 9), (9, 9, 9), (4, 4, 0))
+    nW = (vol[0] // ws[0]) * (vol[1] // ws[1]) * (vol[2] // ws[2])
+    N = ws[0] * ws[1] * ws[2]
+    B, H = nW * 2, 2
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3400 + N)
+    rows = (2 * ws[0] - 1) * (2 * ws[1] - 1) * (2 * ws[2] - 1)
+    bias = bias_from_table(trunc_normal_table(rows, H, 3401 + N), ws).to(dtype)
+    m = oracle.attn_mask(*vol, ws, ss, "float32")
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m, None, scale=0.25)
+    out = fused_swin_attention_shifted(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), vol, ws, ss, scale=0.25)
+    _compare(out, ref, dtype, f"region Dh={Dh} N={N} {dtype}")
+
+
+@pytest.mark.parametrize("N", [513, 729, 1000])
+def test_head_dim_16_beyond_512_tokens(oracle, dev, N):
+    """N above the tuned kernel's 512 runs the general kernel: fp32 mask
+    with boundary flags, fp32 bias."""
+    dtype = torch.float16
+    B, H, Dh = 3, 2, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3500 + N)
+    bias = seeded((H, N, N), torch.float32, 3510 + N) * 0.1
+    mask = torch.where(seeded((B, N, N), torch.float32, 3520 + N) > 0.7, -100.0, 0.0)
+    bnd = torch.tensor([1, 0, 1], dtype=torch.uint8)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), mask.numpy(), bnd.numpy(), scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), bnd.to(dev),
+                               scale=0.25)
+    _compare(out, ref, dtype, f"N={N}")
+
+
+def test_unsupported_head_dim_raises(dev):
+    q = torch.zeros((2, 1, 27, 24), dtype=torch.float16, device=dev)
+    bias = torch.zeros((1, 27, 27), device=dev)
+    with pytest.raises(RuntimeError, match="head_dim 24"):
+        fused_swin_attention(q, q, q, bias, None)
+
+
+@pytest.fixture
+def patched():
+    crumpet_amd.unpatch_monai_swin_unetr()
+    yield
+    crumpet_amd.unpatch_monai_swin_unetr()
+
+
+@pytest.mark.parametrize("fused_block", ["1", "0"], ids=["unfused-block", "fused-block"])
+def test_patched_basic_layer_head_dim_32(patched, dev, monkeypatch, fused_block):
+    """Feature size 96 (head dim 32): the patched BasicLayer (shifted and
+    unshifted blocks) matches its own eager fp32 forward, through the fused
+    block kernels and through partition / attention / unpartition."""
+    from crumpet_amd import fused_block as fb
+    from crumpet_amd import monai_patch
+
+    monkeypatch.setenv("CRUMPET_DISABLE_FUSED_BLOCK", fused_block)
+    calls = []
+    for mod in (monai_patch, fb):
+        for name in ("fused_swin_attention_windows", "fused_swin_attention_shifted"):
+            real = getattr(mod, name)
+
+            def spy(*args, _real=real, _name=name, **kw):
+                calls.append(_name)
+                return _real(*args, **kw)
+
+            monkeypatch.setattr(mod, name, spy)
+    torch.manual_seed(3600)
+    layer = sw.BasicLayer(dim=96, depth=2, num_heads=3, window_size=(7, 7, 7), drop_path=0.0, qkv_bias=True,
+                          downsample=None).to(dev).eval()
+    x = torch.randn((2, 96, 12, 12, 12), generator=torch.Generator().manual_seed(3601)).to(dev)
+    with torch.no_grad():
+        want = layer(x)
+        assert crumpet_amd.patch_monai_swin_unetr()
+        got = layer(x)
+    err = (got - want).abs().max().item()
+    print(f"head dim 32 basic layer: max-abs {err:.2e}, kernel calls {calls}", flush=True)
+    assert calls == ["fused_swin_attention_windows", "fused_swin_attention_shifted"]
+    assert err < 1e-4

@@ -87,7 +87,7 @@ def test_attention_argument_checks_need_no_gpu():
             mask, 1, mb, s3, None, ctypes.c_float(0.25), None)
 
     assert call(Dh=8) == 2
-    assert call(N=600) == 2
+    assert call(Dh=24) == 2 and b"head_dim 24" in lib.crumpet_last_error()
     assert call(dtype=5) == 1
     assert call(mask=fake, mb=3) == 1  # mask batch must divide B
     assert call(B=0) == 0
@@ -101,6 +101,8 @@ def test_attention_argument_checks_need_no_gpu():
     assert shifted(ss=7) == 1 and b"shift" in lib.crumpet_last_error()
     assert shifted(N=216) == 1 and b"window volume" in lib.crumpet_last_error()
     assert shifted(B=6) == 1 and b"multiple" in lib.crumpet_last_error()
+    # the general kernel's region mode holds one class byte per token in LDS
+    assert shifted(N=13 ** 3, D=26, ws=13) == 2 and b"exceed" in lib.crumpet_last_error()
 
 
 def test_window_projection_argument_checks_need_no_gpu():
