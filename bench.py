@@ -215,6 +215,66 @@ def bench_attention(args, dev):
     return res
 
 
+def bench_attention_wide(args, dev):
+    """Head dim 32 (Swin UNETR at feature size 96) at the config-3 window
+    shape: 1372 windows x 3 heads, N = 343, fp16, through the general kernel,
+    shifted (region) and with the mask tensor, against the eager chain."""
+    import torch
+
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
+
+    B, H, N, Dh = C3["B"], C3["H"], C3["N"], 32
+    R = 2  # 2 x 361 MB rotating sets > 256 MB MALL
+    _, bias, mask, bnd = c3_inputs(dev, 0)
+    qkvs = [seeded((B, N, 3 * H * Dh), torch.float16, 320 + r).to(dev) for r in range(R)]
+    views = [q.reshape(B, N, 3, H, Dh).permute(2, 0, 3, 1, 4) for q in qkvs]
+    outs = [torch.empty((B, N, H * Dh), dtype=torch.float16, device=dev) for _ in range(R)]
+    ovs = [o.view(B, N, H, Dh).permute(0, 2, 1, 3) for o in outs]
+
+    def shifted(i):
+        t = views[i % R]
+        fused_swin_attention_shifted(t[0], t[1], t[2], bias, (C3["D"],) * 3, (7, 7, 7), (3, 3, 3), 0.25,
+                                     ovs[i % R])
+
+    def tensor(i):
+        t = views[i % R]
+        fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ovs[i % R])
+
+    steps = max(5, args.steps // 4)
+    _events_time(shifted, 3)
+    res = {"t_shift": _events_time(shifted, steps)}
+    _events_time(tensor, 3)
+    res["t_tensor"] = _events_time(tensor, steps)
+    t = views[0]
+    idx = torch.arange(0, B, 7, device=dev)
+    qf, kf, vf = (t[j][idx].float() for j in range(3))
+    s = (qf * 0.25) @ kf.transpose(-1, -2).contiguous() + bias.float()[None]
+    mb = (mask.float()[idx % mask.shape[0]] * bnd[idx].float()[:, None, None])[:, None]
+    ref = torch.softmax(s + mb, dim=-1) @ vf
+    err = 0.0
+    for fn in (shifted, tensor):
+        fn(0)
+        torch.cuda.synchronize()
+        err = max(err, float((ovs[0][idx].float() - ref).abs().max()))
+    res["max_abs_err"] = err
+    del qf, kf, vf, s, mb, ref
+    if not args.no_eager:
+        def eager(i):
+            tt = views[i % R]
+            a = (tt[0] * 0.25) @ tt[1].transpose(-2, -1).contiguous()
+            a = a + bias.unsqueeze(0)
+            nw = mask.shape[0]
+            a = a.view(B // nw, nw, H, N, N) + mask.unsqueeze(1).unsqueeze(0)
+            a = torch.softmax(a.view(-1, H, N, N), dim=-1)
+            return (a @ tt[2]).transpose(1, 2).reshape(B, N, H * Dh)
+
+        with torch.no_grad():
+            _events_time(eager, 2)
+            res["t_eager"] = _events_time(eager, 5)
+    torch.cuda.empty_cache()
+    return res
+
+
 STAGES = [  # config 4: (name, padded dim, C, heads, window, shift)
     ("s1", 28, 96, 6, (7, 7, 7), (3, 3, 3)),
     ("s2", 14, 192, 12, (7, 7, 7), (3, 3, 3)),
@@ -693,6 +753,8 @@ def main():
     torch.cuda.empty_cache()
     a = {} if args.no_attention else bench_attention(args, dev)
     torch.cuda.empty_cache()
+    aw = {} if args.no_attention else bench_attention_wide(args, dev)
+    torch.cuda.empty_cache()
     blocks = {} if args.no_blocks else bench_blocks(args, dev)
     torch.cuda.empty_cache()
     fused = {} if args.no_fused_block else bench_fused_block(args, dev)
@@ -736,6 +798,20 @@ def main():
         if "t_eager" in a:
             comp_s["speedup_vs_eager"] = round(a["t_eager"] / a["t_shift"], 2)
         components["attention_shifted"] = comp_s
+    if aw:
+        flops = 2 * C3_FLOPS  # head dim 32
+        comp_w = {"workload": "head dim 32 (feature size 96) at the config-3 window shape: 1372 windows x "
+                              "3 heads, N=343, fp16; general kernel",
+                  "flops": flops, "max_abs_err_vs_fp32": aw["max_abs_err"]}
+        for key, t in (("shifted", aw["t_shift"]), ("tensor_mask", aw["t_tensor"])):
+            tfl = flops / (t * 1e-3) / 1e12
+            comp_w[key] = {"ms": round(t, 5), "TFLOP_s": round(tfl, 2),
+                           "frac_mfma_f16": round(tfl / MFMA_F16_PEAK_TFLOPS, 4)}
+            if "t_eager" in aw:
+                comp_w[key]["speedup_vs_eager"] = round(aw["t_eager"] / t, 2)
+        if "t_eager" in aw:
+            comp_w["eager_rocm_ms"] = round(aw["t_eager"], 4)
+        components["attention_hd32"] = comp_w
     if blocks:
         components["block_path"] = blocks
     if fused:

@@ -172,6 +172,21 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.B = static_cast<int32_t>(B);
     p.H = static_cast<int32_t>(Hh);
     p.N = static_cast<int32_t>(N);
+    // 4-element vector IO needs unit d stride, 4-element aligned row strides and bases.
+    bool vec = true;
+    const int64_t* st[4] = {q_strides, k_strides, v_strides, out_strides};
+    const void* ptr[4] = {q, k, v, out};
+    for (int i = 0; i < 4; ++i) {
+        if (st[i][3] != 1 || st[i][0] % 4 || st[i][1] % 4 || st[i][2] % 4 ||
+            reinterpret_cast<uintptr_t>(ptr[i]) % (4 * esize))
+            vec = false;
+    }
+    // the vector staging addresses q/k/v rows of one window with 32-bit byte offsets
+    for (int i = 0; i < 3; ++i) {
+        if (st[i][2] < 0 || ((N - 1) * st[i][2] + 16) * esize >= (int64_t(1) << 31)) vec = false;
+    }
+    p.vec_io = vec ? 1 : 0;
+
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int kmask = region != nullptr                  ? attn::kMaskRegion
                       : mask == nullptr                  ? attn::kNoMask
@@ -197,20 +212,6 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.chunks = static_cast<uint32_t>(chunks);
     p.launched = xcd_launch_count(p.chunks);
 
-    // 4-element vector IO needs unit d stride, 4-element aligned row strides and bases.
-    bool vec = true;
-    const int64_t* st[4] = {q_strides, k_strides, v_strides, out_strides};
-    const void* ptr[4] = {q, k, v, out};
-    for (int i = 0; i < 4; ++i) {
-        if (st[i][3] != 1 || st[i][0] % 4 || st[i][1] % 4 || st[i][2] % 4 ||
-            reinterpret_cast<uintptr_t>(ptr[i]) % (4 * esize))
-            vec = false;
-    }
-    // the vector staging addresses q/k/v rows of one window with 32-bit byte offsets
-    for (int i = 0; i < 3; ++i) {
-        if (st[i][2] < 0 || ((N - 1) * st[i][2] + 16) * esize >= (int64_t(1) << 31)) vec = false;
-    }
-    p.vec_io = vec ? 1 : 0;
 
     if (dtype == CRUMPET_DTYPE_F16)
         attn::launch_f16(p, NT, kmask, s);

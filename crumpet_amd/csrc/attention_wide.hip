@@ -12,14 +12,18 @@
 // the steps of torch-ext/crumpet/fused_attention.py:82-146 in the reference.
 //
 // Decomposition: a workgroup of 4 waves owns one (window, head) and 64
-// queries (a 16-query strip per wave); it walks the keys in chunks of 64,
-// staging K (row-major) and V^T in LDS, and keeps the strip's Q fragments,
-// the online-softmax state and the O^T accumulators in registers.  Per
-// 16-key tile: S^T = K Q^T on the matrix cores over D/16 16-dim steps,
-// starting from the bias (+ mask) tile; per chunk one online-softmax update;
-// then O^T += V^T P^T with P straight from the score registers (the score
-// tile's layout is the B-operand layout).  Bias and mask are read as floats
-// of their own dtype with their own strides.  Nothing is allocated.
+// queries (a 16-query strip per wave); it walks the keys in chunks of 64
+// (32 from head dim 64 up, for registers),
+// with K (row-major) and V^T double-buffered in LDS, and keeps the strip's Q
+// fragments, the online-softmax state and the O^T accumulators in
+// registers.  The next chunk's K/V rows and bias (+ mask) values are
+// requested into registers before the current chunk is computed, so their
+// latency overlaps the compute; one barrier per chunk.  Per 16-key tile:
+// S^T = K Q^T on the matrix cores over D/16 16-dim steps, starting from the
+// bias (+ mask) tile; per chunk one online-softmax update; then
+// O^T += V^T P^T with P straight from the score registers (the score tile's
+// layout is the B-operand layout).  Bias and mask are read as floats of
+// their own dtype with their own strides.  Nothing is allocated.
 #include <hip/hip_runtime.h>
 
 #include <math.h>
@@ -34,7 +38,6 @@ namespace {
 
 constexpr int kWideThreads = 256;
 constexpr int kWideWaves = 4;
-constexpr int kKeyChunk = 64;  // keys staged per LDS chunk
 constexpr float kWideLog2e = 1.4426950408889634f;
 
 typedef float f32x4w __attribute__((ext_vector_type(4)));
@@ -79,6 +82,71 @@ __device__ __forceinline__ float load_as_float(const void* base, int64_t i, int3
     return static_cast<float>(static_cast<const __bf16*>(base)[i]);
 }
 
+// Elements d0..d0+3 of a row with element stride sd: one vector access
+// when the row has unit stride and 4-element alignment (vec), else four.
+template <typename T>
+__device__ __forceinline__ auto load4v(const T* row, int d0, int64_t sd, bool vec) {
+    typedef T V4 __attribute__((ext_vector_type(4)));
+    if (vec) return *reinterpret_cast<const V4*>(row + d0);
+    V4 v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = row[int64_t(d0 + r) * sd];
+    return v;
+}
+
+template <typename T, typename V4>
+__device__ __forceinline__ void store4v(T* row, int d0, int64_t sd, bool vec, V4 v) {
+    if (vec) {
+        *reinterpret_cast<V4*>(row + d0) = v;
+        return;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) row[int64_t(d0 + r) * sd] = v[r];
+}
+
+// The lane's bias (+ mask) values of keys kc0 + 16 t + 4 g + r of a chunk
+// (t < kKC / 16, r < 4) as floats; keys past N read key N - 1 and become
+// -inf.  Branch-free inside: TB / TM are the bias / mask element types.
+template <typename TB, typename TM, int kKC>
+__device__ __forceinline__ void fetch_bias_rows(float (&bq)[kKC / 4], const void* bias_row, const void* mask_row,
+                                                int kc0, int g, int N) {
+    const TB* brow = static_cast<const TB*>(bias_row);
+    const TM* mrow = static_cast<const TM*>(mask_row);
+#pragma unroll
+    for (int t = 0; t < kKC / 16; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int k0 = kc0 + 16 * t + 4 * g + r;
+            const int kk = min(k0, N - 1);
+            float bv = static_cast<float>(brow[kk]);
+            if (mrow != nullptr) bv += static_cast<float>(mrow[kk]);
+            bq[4 * t + r] = k0 < N ? bv : -INFINITY;
+        }
+}
+
+template <typename TB, int kKC>
+__device__ __forceinline__ void fetch_bias_m(float (&bq)[kKC / 4], const void* bias_row, const void* mask_row,
+                                             int32_t mdt, int kc0, int g, int N) {
+    if (mask_row == nullptr || mdt == CRUMPET_DTYPE_F32)
+        fetch_bias_rows<TB, float, kKC>(bq, bias_row, mask_row, kc0, g, N);
+    else if (mdt == CRUMPET_DTYPE_F16)
+        fetch_bias_rows<TB, _Float16, kKC>(bq, bias_row, mask_row, kc0, g, N);
+    else
+        fetch_bias_rows<TB, __bf16, kKC>(bq, bias_row, mask_row, kc0, g, N);
+}
+
+// Dispatch on the (uniform) bias dtype; mask_row null = no mask.
+template <typename Unused, int kKC>
+__device__ __forceinline__ void fetch_bias_any(float (&bq)[kKC / 4], const void* bias_row, int32_t bdt,
+                                               const void* mask_row, int32_t mdt, int kc0, int g, int N) {
+    if (bdt == CRUMPET_DTYPE_F32)
+        fetch_bias_m<float, kKC>(bq, bias_row, mask_row, mdt, kc0, g, N);
+    else if (bdt == CRUMPET_DTYPE_F16)
+        fetch_bias_m<_Float16, kKC>(bq, bias_row, mask_row, mdt, kc0, g, N);
+    else
+        fetch_bias_m<__bf16, kKC>(bq, bias_row, mask_row, mdt, kc0, g, N);
+}
+
 // kMode: 0 no mask, 1 mask tensor (mask[b mod mask_batch], skipped where a
 // boundary flag is 0), 2 shifted-window regions of the [D, H, W] volume.
 template <typename T, int D, int kMode>
@@ -88,11 +156,15 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
     typedef WideMma<T> M;
     typedef typename M::x4 X4;
     constexpr int kDC = D / 16;                                 // 16-dim steps
+    constexpr int kKC = D <= 32 ? 64 : 32;                      // keys per chunk (registers of the prefetch)
     constexpr int kPad = 16 / static_cast<int>(sizeof(T));      // 16 bytes per LDS row
     constexpr int kKStride = D + kPad;                          // K row stride (elements)
-    constexpr int kVStride = kKeyChunk + kPad;                  // V^T row stride (elements)
-    __shared__ __attribute__((aligned(16))) T k_lds[kKeyChunk * kKStride];
-    __shared__ __attribute__((aligned(16))) T vt_lds[D * kVStride];
+    constexpr int kVStride = kKC + kPad;                  // V^T row stride (elements)
+    constexpr int kUnits = kKC * (D / 4) / kWideThreads;  // 4-element K/V units per thread and chunk
+    static_assert(kUnits >= 1 && kKC * (D / 4) % kWideThreads == 0, "chunk units per thread");
+    typedef T V4 __attribute__((ext_vector_type(4)));
+    __shared__ __attribute__((aligned(16))) T k_lds[2][kKC * kKStride];
+    __shared__ __attribute__((aligned(16))) T vt_lds[2][D * kVStride];
     __shared__ uint8_t cls_lds[kMode == 2 ? kWideMaxRegionN : 4];
 
     uint32_t chunk;
@@ -148,78 +220,121 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
 
     // B operand of S^T = K Q^T: Q[qr][16 dc + 4 g + r], scaled in fp32 and
     // rounded back to T
+    const bool vec = p.vec_io != 0;  // unit d stride, 4-element aligned rows and bases
     const T* qrow = static_cast<const T*>(p.q) + int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1] +
                     int64_t(qr) * p.qs[2];
     X4 qf[kDC];
 #pragma unroll
-    for (int dc = 0; dc < kDC; ++dc)
+    for (int dc = 0; dc < kDC; ++dc) {
+        const V4 qv = load4v(qrow, 16 * dc + 4 * g, p.qs[3], vec);
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-            qf[dc][r] = static_cast<T>(static_cast<float>(qrow[int64_t(16 * dc + 4 * g + r) * p.qs[3]]) * p.scale);
+        for (int r = 0; r < 4; ++r) qf[dc][r] = static_cast<T>(static_cast<float>(qv[r]) * p.scale);
+    }
 
     const T* kbase = static_cast<const T*>(p.k) + int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1];
     const T* vbase = static_cast<const T*>(p.v) + int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1];
+
+    // K and V rows of the next key chunk travel through registers: they are
+    // requested before the current chunk is computed and written to the
+    // other LDS buffer after it, so the loads overlap the compute.  Thread
+    // unit e covers key e / (D / 4), dims 4 (e mod (D / 4)) .. + 3.
+    V4 kr[kUnits], vr[kUnits];
+    // Keys past N re-read row N - 1: their scores are -inf (bias) and their
+    // P is 0, so any finite K/V row serves, and no branch is needed.
+    auto fetch_kv = [&](int kc0) {
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) {
+            const int e = threadIdx.x + u * kWideThreads;
+            const int kk = min(kc0 + e / (D / 4), N - 1);
+            const int d0 = (e % (D / 4)) * 4;
+            kr[u] = load4v(kbase + int64_t(kk) * p.ks[2], d0, p.ks[3], vec);
+            vr[u] = load4v(vbase + int64_t(kk) * p.vs[2], d0, p.vs[3], vec);
+        }
+    };
+    auto stash_kv = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < kUnits; ++u) {
+            const int e = threadIdx.x + u * kWideThreads;
+            const int key = e / (D / 4);
+            const int d0 = (e % (D / 4)) * 4;
+            *reinterpret_cast<V4*>(&k_lds[buf][key * kKStride + d0]) = kr[u];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) vt_lds[buf][(d0 + r) * kVStride + key] = vr[u][r];
+        }
+    };
+    // bias (+ mask tensor) of the lane's scores of a chunk, also one chunk
+    // ahead; keys past N read key N - 1 and become -inf (no branches: the
+    // dtype choice is uniform and outside the loops)
+    float bq[kKC / 4];
+    auto fetch_bias = [&](int kc0) __attribute__((always_inline)) {
+        const int bdt = p.bias_dtype;
+        if constexpr (kMode == 1) {
+            if (!use_mask)
+                fetch_bias_any<float, kKC>(bq, bias_row, bdt, nullptr, 0, kc0, g, N);
+            else
+                fetch_bias_any<float, kKC>(bq, bias_row, bdt, mask_row, mask_dtype, kc0, g, N);
+        } else {
+            fetch_bias_any<float, kKC>(bq, bias_row, bdt, nullptr, 0, kc0, g, N);
+        }
+    };
 
     f32x4w o[kDC];  // O^T: o[dd][r] = O[query col][16 dd + 4 g + r]
 #pragma unroll
     for (int dd = 0; dd < kDC; ++dd) o[dd] = f32x4w{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -INFINITY;
     float l_part = 0.0f;  // this lane's share of the row sum (its keys 4g..4g+3 of each tile)
-    int my_cls = 0;  // region class of this lane's query (region mode)
 
-    for (int kc0 = 0; kc0 < N; kc0 += kKeyChunk) {
-        __syncthreads();  // the previous chunk's LDS reads are done (first: the class table is written)
-        if constexpr (kMode == 2)
-            if (kc0 == 0) my_cls = cls_lds[qr];
-        // stage K rows and V^T of keys kc0..kc0+63 (zeros past N)
-        for (int e = threadIdx.x; e < kKeyChunk * (D / 4); e += kWideThreads) {
-            const int key = e / (D / 4);
-            const int d0 = (e % (D / 4)) * 4;
-            const int kk = kc0 + key;
+    fetch_kv(0);
+    fetch_bias(0);
+    stash_kv(0);
+    __syncthreads();  // chunk 0 and (region mode) the class table are in LDS
+    int my_cls = 0;   // region class of this lane's query
+    if constexpr (kMode == 2) my_cls = cls_lds[qr];
+
+    const int nchunks = (N + kKC - 1) / kKC;
+    for (int c = 0; c < nchunks; ++c) {
+        const int kc0 = c * kKC;
+        const int buf = c & 1;
+        const bool more = c + 1 < nchunks;
+        float bc[kKC / 4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                T kv = static_cast<T>(0.0f), vv = static_cast<T>(0.0f);
-                if (kk < N) {
-                    kv = kbase[int64_t(kk) * p.ks[2] + int64_t(d0 + r) * p.ks[3]];
-                    vv = vbase[int64_t(kk) * p.vs[2] + int64_t(d0 + r) * p.vs[3]];
-                }
-                k_lds[key * kKStride + d0 + r] = kv;
-                vt_lds[(d0 + r) * kVStride + key] = vv;
-            }
+        for (int i = 0; i < kKC / 4; ++i) bc[i] = bq[i];
+        if (more) {
+            fetch_kv(kc0 + kKC);
+            fetch_bias(kc0 + kKC);
         }
-        __syncthreads();
 
         // scores of the chunk's 4 key tiles: lane (col, g) holds
         // S[query col][key kc0 + 16 t + 4 g + r]
-        f32x4w S[kKeyChunk / 16];
+        f32x4w S[kKC / 16];
 #pragma unroll
-        for (int t = 0; t < kKeyChunk / 16; ++t) {
-            f32x4w c;
+        for (int t = 0; t < kKC / 16; ++t) {
+            f32x4w acc;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int kk = kc0 + 16 * t + 4 * g + r;
-                float bv = -INFINITY;
-                if (kk < N) {
-                    bv = load_as_float(bias_row, kk, p.bias_dtype);
-                    if constexpr (kMode == 1)
-                        if (use_mask) bv += load_as_float(mask_row, kk, mask_dtype);
-                    if constexpr (kMode == 2)
-                        if ((my_cls ^ cls_lds[kk]) & split) bv += -100.0f;
+                acc[r] = bc[4 * t + r];
+            }
+            if constexpr (kMode == 2) {
+                if (split != 0) {  // windows not last along a shifted axis see no mask
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int kk = min(kc0 + 16 * t + 4 * g + r, N - 1);
+                        acc[r] += ((my_cls ^ cls_lds[kk]) & split) ? -100.0f : 0.0f;
+                    }
                 }
-                c[r] = bv;
             }
 #pragma unroll
             for (int dc = 0; dc < kDC; ++dc) {
-                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[(16 * t + col) * kKStride + 16 * dc + 4 * g]);
-                c = M::step(kf, qf[dc], c);
+                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[buf][(16 * t + col) * kKStride + 16 * dc + 4 * g]);
+                acc = M::step(kf, qf[dc], acc);
             }
-            S[t] = c;
+            S[t] = acc;
         }
 
         // online softmax over the chunk: row max across the 4 lane groups
         float cm = -INFINITY;
 #pragma unroll
-        for (int t = 0; t < kKeyChunk / 16; ++t)
+        for (int t = 0; t < kKC / 16; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) cm = fmaxf(cm, S[t][r]);
         cm = fmaxf(cm, __shfl_xor(cm, 16));
@@ -234,7 +349,7 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
         const float mb = m_use * kWideLog2e;
 
 #pragma unroll
-        for (int t = 0; t < kKeyChunk / 16; ++t) {
+        for (int t = 0; t < kKC / 16; ++t) {
             X4 pb;
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -245,10 +360,14 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
             // O^T += V^T P^T: A = V^T[16 dd + col][keys 16 t + 4 g ..], B = P^T
 #pragma unroll
             for (int dd = 0; dd < kDC; ++dd) {
-                const X4 vf = *reinterpret_cast<const X4*>(&vt_lds[(16 * dd + col) * kVStride + 16 * t + 4 * g]);
+                const X4 vf =
+                    *reinterpret_cast<const X4*>(&vt_lds[buf][(16 * dd + col) * kVStride + 16 * t + 4 * g]);
                 o[dd] = M::step(vf, pb, o[dd]);
             }
         }
+        // the other buffer was last read before the previous barrier
+        if (more) stash_kv(buf ^ 1);
+        __syncthreads();
     }
 
     float l = l_part;
@@ -257,9 +376,12 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
     if (qi < N) {
         T* orow = static_cast<T*>(p.out) + int64_t(b) * p.os[0] + int64_t(h) * p.os[1] + int64_t(qi) * p.os[2];
 #pragma unroll
-        for (int dd = 0; dd < kDC; ++dd)
+        for (int dd = 0; dd < kDC; ++dd) {
+            V4 ov;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) orow[int64_t(16 * dd + 4 * g + r) * p.os[3]] = static_cast<T>(o[dd][r] / l);
+            for (int r = 0; r < 4; ++r) ov[r] = static_cast<T>(o[dd][r] / l);
+            store4v(orow, 16 * dd + 4 * g, p.os[3], vec, ov);
+        }
     }
 }
 

@@ -174,7 +174,10 @@ CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  *
  * Needs no workspace: every buffer is an input or the output.
  *
- * Supported: Dh = 16, 1 <= N <= 512.
+ * Supported: Dh = 16, 32, 64 or 128 and any N >= 1.  Dh = 16 with N <= 512
+ * (every Swin UNETR stage at feature size 48) runs the tuned kernel; other
+ * shapes run the general kernel, whose shifted-window mode below takes
+ * windows of up to 2048 tokens.
  *
  * Replaces the Triton launch of `_fused_swin_attention_kernel`,
  * torch-ext/crumpet/fused_attention.py:48-146 (wrapper :149-226).  The
