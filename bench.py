@@ -691,6 +691,15 @@ def profile_run(dev):
           lambda i: fused_swin_attention_shifted(views[i % 3][0], views[i % 3][1], views[i % 3][2], bias, vol,
                                                  (7, 7, 7), (3, 3, 3), 0.25, ov))
     del qkvs, views, o, ov, mask
+    # the general kernel: head dim 32 at the same window shape, shifted mode
+    qkvs = [seeded((Bw, N, 3 * Hh * 32), torch.float16, 320 + r).to(dev) for r in range(2)]
+    views = [q.reshape(Bw, N, 3, Hh, 32).permute(2, 0, 3, 1, 4) for q in qkvs]
+    o = torch.empty((Bw, N, Hh * 32), dtype=torch.float16, device=dev)
+    ov = o.view(Bw, N, Hh, 32).permute(0, 2, 1, 3)
+    timed("attention_hd32_shifted",
+          lambda i: fused_swin_attention_shifted(views[i % 2][0], views[i % 2][1], views[i % 2][2], bias, vol,
+                                                 (7, 7, 7), (3, 3, 3), 0.25, ov))
+    del qkvs, views, o, ov
 
     # fused block projections at the config-5 stage-0 shape: fp32 block
     # input [4,48^3,48] -> fp16 qkv [1372,343,144]; fp16 attention output
