@@ -104,6 +104,31 @@ def test_head_dim_32_strided_qkv_views_and_strided_out(oracle, dev, dtype):
     _compare(out, ref, dtype, f"strided {dtype}")
 
 
+@pytest.mark.parametrize("Dh", [32, 64])
+def test_non_unit_d_stride_and_odd_offsets(oracle, dev, Dh):
+    """q/k/v stored [B, H, D, N] and read through a transposed view (d stride
+    N), out written through a transposed view, and a 2-element offset that
+    breaks 4-element alignment: the general kernel's element-wise path."""
+    dtype = torch.float16
+    B, H, N = 4, 2, 125
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3700 + Dh)
+    bias = seeded((H, N, N), torch.float32, 3710) * 0.1
+
+    def transposed(t):
+        buf = torch.empty((B * H * N * Dh + 2,), dtype=dtype, device=dev)
+        view = buf[2:].view(B, H, Dh, N)
+        view.copy_(t.to(dev).transpose(-1, -2))
+        return view.transpose(-1, -2)
+
+    qd, kd, vd = transposed(q), transposed(k), transposed(v)
+    assert qd.stride(-1) == N
+    obuf = torch.empty((B * H * N * Dh + 2,), dtype=dtype, device=dev)
+    out = obuf[2:].view(B, H, Dh, N).transpose(-1, -2)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=0.25)
+    fused_swin_attention(qd, kd, vd, bias.to(dev), None, scale=0.25, out=out)
+    _compare(out, ref, dtype, f"non-unit d stride Dh={Dh}")
+
+
 @pytest.mark.parametrize("Dh", [16, 32])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_shifted_regions_general_kernel(oracle, dev, Dh, dtype):
