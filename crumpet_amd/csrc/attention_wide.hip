@@ -105,47 +105,63 @@ __device__ __forceinline__ void store4v(T* row, int d0, int64_t sd, bool vec, V4
     for (int r = 0; r < 4; ++r) row[int64_t(d0 + r) * sd] = v[r];
 }
 
+// One element of type T at byte offset off of a buffer resource, as a
+// float (offsets past the resource's extent read 0).
+template <typename T>
+__device__ __forceinline__ float buffer_elem(__amdgpu_buffer_rsrc_t rs, int off) {
+    if constexpr (sizeof(T) == 4) {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+    } else {
+        const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+        return static_cast<float>(__builtin_bit_cast(T, h));
+    }
+}
+
 // The lane's bias (+ mask) values of keys kc0 + 16 t + 4 g + r of a chunk
-// (t < kKC / 16, r < 4) as floats; keys past N read key N - 1 and become
-// -inf.  Branch-free inside: TB / TM are the bias / mask element types.
+// (t < kKC / 16, r < 4) as floats, through buffer resources spanning the
+// head's bias and the window's mask; boff / moff are the lane's row
+// offsets in bytes.  Keys past N become -inf (their loads read the next row
+// or 0).  TB / TM are the bias / mask element types; the key offsets are
+// instruction immediates.
 template <typename TB, typename TM, int kKC>
-__device__ __forceinline__ void fetch_bias_rows(float (&bq)[kKC / 4], const void* bias_row, const void* mask_row,
-                                                int kc0, int g, int N) {
-    const TB* brow = static_cast<const TB*>(bias_row);
-    const TM* mrow = static_cast<const TM*>(mask_row);
+__device__ __forceinline__ void fetch_bias_rows(float (&bq)[kKC / 4], __amdgpu_buffer_rsrc_t brs, int boff,
+                                                __amdgpu_buffer_rsrc_t mrs, int moff, bool use_mask, int kc0,
+                                                int g, int N) {
+    const int k4 = kc0 + 4 * g;
 #pragma unroll
     for (int t = 0; t < kKC / 16; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int k0 = kc0 + 16 * t + 4 * g + r;
-            const int kk = min(k0, N - 1);
-            float bv = static_cast<float>(brow[kk]);
-            if (mrow != nullptr) bv += static_cast<float>(mrow[kk]);
+            const int k0 = k4 + 16 * t + r;
+            float bv = buffer_elem<TB>(brs, boff + k4 * int(sizeof(TB)) + (16 * t + r) * int(sizeof(TB)));
+            if (use_mask) bv += buffer_elem<TM>(mrs, moff + k4 * int(sizeof(TM)) + (16 * t + r) * int(sizeof(TM)));
             bq[4 * t + r] = k0 < N ? bv : -INFINITY;
         }
 }
 
 template <typename TB, int kKC>
-__device__ __forceinline__ void fetch_bias_m(float (&bq)[kKC / 4], const void* bias_row, const void* mask_row,
-                                             int32_t mdt, int kc0, int g, int N) {
-    if (mask_row == nullptr || mdt == CRUMPET_DTYPE_F32)
-        fetch_bias_rows<TB, float, kKC>(bq, bias_row, mask_row, kc0, g, N);
+__device__ __forceinline__ void fetch_bias_m(float (&bq)[kKC / 4], __amdgpu_buffer_rsrc_t brs, int boff,
+                                             __amdgpu_buffer_rsrc_t mrs, int moff, bool use_mask, int32_t mdt,
+                                             int kc0, int g, int N) {
+    if (!use_mask || mdt == CRUMPET_DTYPE_F32)
+        fetch_bias_rows<TB, float, kKC>(bq, brs, boff, mrs, moff, use_mask, kc0, g, N);
     else if (mdt == CRUMPET_DTYPE_F16)
-        fetch_bias_rows<TB, _Float16, kKC>(bq, bias_row, mask_row, kc0, g, N);
+        fetch_bias_rows<TB, _Float16, kKC>(bq, brs, boff, mrs, moff, use_mask, kc0, g, N);
     else
-        fetch_bias_rows<TB, __bf16, kKC>(bq, bias_row, mask_row, kc0, g, N);
+        fetch_bias_rows<TB, __bf16, kKC>(bq, brs, boff, mrs, moff, use_mask, kc0, g, N);
 }
 
-// Dispatch on the (uniform) bias dtype; mask_row null = no mask.
-template <typename Unused, int kKC>
-__device__ __forceinline__ void fetch_bias_any(float (&bq)[kKC / 4], const void* bias_row, int32_t bdt,
-                                               const void* mask_row, int32_t mdt, int kc0, int g, int N) {
+// Dispatch on the (uniform) bias dtype.
+template <int kKC>
+__device__ __forceinline__ void fetch_bias_any(float (&bq)[kKC / 4], __amdgpu_buffer_rsrc_t brs, int32_t bdt,
+                                               int boff, __amdgpu_buffer_rsrc_t mrs, int moff, bool use_mask,
+                                               int32_t mdt, int kc0, int g, int N) {
     if (bdt == CRUMPET_DTYPE_F32)
-        fetch_bias_m<float, kKC>(bq, bias_row, mask_row, mdt, kc0, g, N);
+        fetch_bias_m<float, kKC>(bq, brs, boff, mrs, moff, use_mask, mdt, kc0, g, N);
     else if (bdt == CRUMPET_DTYPE_F16)
-        fetch_bias_m<_Float16, kKC>(bq, bias_row, mask_row, mdt, kc0, g, N);
+        fetch_bias_m<_Float16, kKC>(bq, brs, boff, mrs, moff, use_mask, mdt, kc0, g, N);
     else
-        fetch_bias_m<__bf16, kKC>(bq, bias_row, mask_row, mdt, kc0, g, N);
+        fetch_bias_m<__bf16, kKC>(bq, brs, boff, mrs, moff, use_mask, mdt, kc0, g, N);
 }
 
 // kMode: 0 no mask, 1 mask tensor (mask[b mod mask_batch], skipped where a
@@ -207,17 +223,25 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
         split = ((wd == p.nWd - 1 && p.ss[0] > 0) ? 4 : 0) | ((wh == p.nWh - 1 && p.ss[1] > 0) ? 2 : 0) |
                 ((ww == p.nWw - 1 && p.ss[2] > 0) ? 1 : 0);
     }
+    // bias and mask rows through buffer resources: the head's bias [N, N]
+    // and the window's mask [N, N] extents (the host checked that they fit
+    // 31 bits); the lane's row offset is a per-lane byte offset
+    const int bsz = p.bias_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(static_cast<const char*>(p.bias) + int64_t(h) * p.bsd[0] * bsz), 0,
+        __builtin_amdgcn_readfirstlane(static_cast<int>((int64_t(N - 1) * p.bsd[1] + N) * bsz)), 0x00020000);
+    const int boff = static_cast<int>(int64_t(qr) * p.bsd[1] * bsz);
     bool use_mask = false;
-    const void* mask_row = nullptr;
+    __amdgpu_buffer_rsrc_t mrs = brs;
+    int moff = 0;
     if constexpr (kMode == 1) {
         use_mask = p.boundary == nullptr || p.boundary[b] != 0;
         const int msz = mask_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
-        mask_row = static_cast<const char*>(p.mask) +
-                   (int64_t(b % p.mask_batch) * p.ms[0] + int64_t(qr) * p.ms[1]) * msz;
+        mrs = __builtin_amdgcn_make_buffer_rsrc(
+            uniform_ptr(static_cast<const char*>(p.mask) + int64_t(b % p.mask_batch) * p.ms[0] * msz), 0,
+            __builtin_amdgcn_readfirstlane(static_cast<int>((int64_t(N - 1) * p.ms[1] + N) * msz)), 0x00020000);
+        moff = static_cast<int>(int64_t(qr) * p.ms[1] * msz);
     }
-    const int bsz = p.bias_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
-    const void* bias_row =
-        static_cast<const char*>(p.bias) + (int64_t(h) * p.bsd[0] + int64_t(qr) * p.bsd[1]) * bsz;
 
     // B operand of S^T = K Q^T: Q[qr][16 dc + 4 g + r], scaled in fp32 and
     // rounded back to T
@@ -264,19 +288,10 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
         }
     };
     // bias (+ mask tensor) of the lane's scores of a chunk, also one chunk
-    // ahead; keys past N read key N - 1 and become -inf (no branches: the
-    // dtype choice is uniform and outside the loops)
+    // ahead (the dtype choice is uniform and outside the loops)
     float bq[kKC / 4];
     auto fetch_bias = [&](int kc0) __attribute__((always_inline)) {
-        const int bdt = p.bias_dtype;
-        if constexpr (kMode == 1) {
-            if (!use_mask)
-                fetch_bias_any<float, kKC>(bq, bias_row, bdt, nullptr, 0, kc0, g, N);
-            else
-                fetch_bias_any<float, kKC>(bq, bias_row, bdt, mask_row, mask_dtype, kc0, g, N);
-        } else {
-            fetch_bias_any<float, kKC>(bq, bias_row, bdt, nullptr, 0, kc0, g, N);
-        }
+        fetch_bias_any<kKC>(bq, brs, p.bias_dtype, boff, mrs, moff, use_mask, mask_dtype, kc0, g, N);
     };
 
     f32x4w o[kDC];  // O^T: o[dd][r] = O[query col][16 dd + 4 g + r]
