@@ -1,8 +1,8 @@
 // General fused window attention for the shapes the head-dim-16 kernel does
 // not cover: head dims 32, 64 and 128, and windows of more than 512 tokens
-// (any head dim of 16..128 that is a power of two, any N).  Same contract,
-// same numerics and the same three mask modes as swin_attention_d16_kernel
-// (attention_kernel.h):
+// (any head dim of 16..128 that is a power of two, any N).  Same contract
+// and the same three mask modes as swin_attention_d16_kernel
+// (attention_kernel.h); the numerics are the reference's:
 //
 //   S = (q * scale) k^T + bias[h] + mask,  out = softmax_rows(S) v
 //
@@ -13,8 +13,8 @@
 //
 // Decomposition: a workgroup of 4 waves owns one (window, head) and 64
 // queries (a 16-query strip per wave); it walks the keys in chunks of 64
-// (32 from head dim 32 up: the smaller prefetch fits 4 waves per SIMD at
-// head dim 32, which was 12% faster than 64-key chunks at 3 waves),
+// (32 from head dim 32 up: the smaller register prefetch raises occupancy,
+// 12% faster than 64-key chunks at head dim 32),
 // with K (row-major) and V^T double-buffered in LDS, and keeps the strip's Q
 // fragments, the online-softmax state and the O^T accumulators in
 // registers.  The next chunk's K/V rows and bias (+ mask) values are
