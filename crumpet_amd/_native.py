@@ -51,9 +51,12 @@ _error: str | None = None
 
 
 def _load() -> None:
+    # Only success is cached: after a failed attempt (e.g. the libraries were
+    # not built yet) the next call tries again.
     global _hip, _ops, _error
-    if _ops is not None or _error is not None:
+    if _ops is not None:
         return
+    _error = None
     try:
         if not HIP_LIB.exists() or not OPS_LIB.exists():
             raise OSError(
