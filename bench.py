@@ -31,6 +31,17 @@ ROOT = Path(__file__).resolve().parent
 if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
+
+def synthetic_ct(shape, seed):
+    """Config-5 input volume; the generator is shared with the test suite."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    try:
+        from helpers import synthetic_ct as make
+    finally:
+        sys.path.remove(str(ROOT / "tests"))
+    return make(shape, seed)
+
+
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 
@@ -444,23 +455,6 @@ def bench_fused_block(args, dev):
         del x, xs, qkv_outs, wins, ys, blk
         torch.cuda.empty_cache()
     return res
-
-
-def synthetic_ct(shape, seed):
-    """Config 5 input: uniform [0,1] intensities plus smooth Gaussian blobs, clamped to [0,1]."""
-    import torch
-
-    g = torch.Generator().manual_seed(seed)
-    b, c, d, h, w = shape
-    vol = torch.rand(shape, generator=g) * 0.5
-    zz, yy, xx = torch.meshgrid(torch.arange(d), torch.arange(h), torch.arange(w), indexing="ij")
-    for _ in range(12):
-        ctr = torch.rand(3, generator=g) * torch.tensor([d, h, w])
-        sigma = 4.0 + 8.0 * torch.rand(1, generator=g).item()
-        amp = 0.3 + 0.5 * torch.rand(1, generator=g).item()
-        r2 = (zz - ctr[0]) ** 2 + (yy - ctr[1]) ** 2 + (xx - ctr[2]) ** 2
-        vol += amp * torch.exp(-r2 / (2 * sigma * sigma))
-    return vol.clamp_(0.0, 1.0)
 
 
 def bench_e2e(args, dev):

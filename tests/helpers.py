@@ -55,6 +55,22 @@ def boundary_flags(D, H, W, ws, ss, outer=1):
     return torch.tensor(flags * outer, dtype=torch.uint8)
 
 
+def synthetic_ct(shape, seed):
+    """Config 5 input: a CT-like volume, uniform intensities in [0, 0.5] plus
+    12 smooth seeded Gaussian blobs, clamped to [0, 1] (float32, CPU)."""
+    g = torch.Generator().manual_seed(seed)
+    b, c, d, h, w = shape
+    vol = torch.rand(shape, generator=g) * 0.5
+    zz, yy, xx = torch.meshgrid(torch.arange(d), torch.arange(h), torch.arange(w), indexing="ij")
+    for _ in range(12):
+        ctr = torch.rand(3, generator=g) * torch.tensor([d, h, w])
+        sigma = 4.0 + 8.0 * torch.rand(1, generator=g).item()
+        amp = 0.3 + 0.5 * torch.rand(1, generator=g).item()
+        r2 = (zz - ctr[0]) ** 2 + (yy - ctr[1]) ** 2 + (xx - ctr[2]) ** 2
+        vol += amp * torch.exp(-r2 / (2 * sigma * sigma))
+    return vol.clamp_(0.0, 1.0)
+
+
 def c_abi():
     """ctypes handle of libcrumpet_hip.so with argument types from include/crumpet_hip.h."""
     from crumpet_amd import _native

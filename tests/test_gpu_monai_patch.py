@@ -160,6 +160,52 @@ def test_patched_swin_unetr_matches_eager_fp32(patched, dev, block_mode):
     assert err < 1e-4 * max(1.0, scale)
 
 
+def _config5_model(dev):
+    torch.manual_seed(123)
+    return sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=48, depths=(2, 2, 2, 2),
+                        num_heads=(3, 6, 12, 24)).to(dev).eval()
+
+
+def test_config5_swin_unetr_fp16_autocast(patched, dev, block_mode):
+    """BASELINE config 5 as the reference benchmarks it
+    (benchmarks/bench_e2e.py:27-53): SwinUNETR(1 -> 14, feature 48, depths
+    2222, heads 3/6/12/24) on a [4,1,96,96,96] fp16 synthetic CT volume under
+    fp16 autocast, patched against the unpatched eager forward of the same
+    weights.  Eager rounds q k^T to fp16 before the bias, the kernels keep
+    the scores in fp32, so the bound is 1e-2 of the largest logit."""
+    from helpers import synthetic_ct
+
+    model = _config5_model(dev)
+    x = synthetic_ct((4, 1, 96, 96, 96), 77).half().to(dev)
+    want = _run(model, x, autocast=True).float()
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(model, x, autocast=True).float()
+    assert got.shape == (4, 14, 96, 96, 96)
+    assert torch.isfinite(got).all()
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    print(f"config 5 fp16 autocast ({block_mode}): max-abs logit delta {err:.2e} "
+          f"(max |logit| {scale:.2f})", flush=True)
+    assert err <= 1e-2 * scale
+
+
+def test_config5_swin_unetr_fp32(patched, dev, block_mode):
+    """Config 5's model and input shape in fp32: the kernels compute in fp32,
+    so patched and eager logits agree to 1e-4 of the largest logit."""
+    from helpers import synthetic_ct
+
+    model = _config5_model(dev)
+    x = synthetic_ct((4, 1, 96, 96, 96), 77).to(dev)
+    want = _run(model, x)
+    assert crumpet_amd.patch_monai_swin_unetr()
+    got = _run(model, x)
+    err = (got - want).abs().max().item()
+    scale = want.abs().max().item()
+    print(f"config 5 fp32 ({block_mode}): max-abs logit delta {err:.2e} (max |logit| {scale:.2f})",
+          flush=True)
+    assert err <= 1e-4 * scale
+
+
 def test_training_mode_falls_back_and_backpropagates(patched, dev):
     torch.manual_seed(9)
     layer = _layer(48, 3, 9, depth=2).to(dev).train()
