@@ -45,14 +45,15 @@
 //   ones^T P^T.  O^T lands as 4 consecutive head-dim values of one query per
 //   lane, which is one 8-byte store.
 //
-// Softmax
-//   Online over key chunks of at most 6 tiles, with a lazy rescale: the
-//   first chunk fixes the row max, later chunks exponentiate against the
-//   running max and refresh it (with a cross-lane reduction and a rescale of
-//   O and the row sums) only when a score exceeds it by more than
-//   kLazyMargin.  The small chunks keep 2-byte vector-IO kernels within 168
-//   VGPRs, i.e. 3 waves per SIMD, which this latency-bound loop needs more
-//   than it needs a larger register budget.
+// Softmax (2-byte types, attend_offset)
+//   Scores are produced in log2 units (Q carries scale * log2(e) as a hi/lo
+//   pair in the 32-deep score product, the bias tiles log2(e)), so P = 2^S
+//   costs one exp and half a conversion per score.  Instead of a row max, the
+//   bias tiles carry a per-query offset, and the exact row sums that the same
+//   pass produces check that every P stayed in the range where its rounding
+//   is as good as with the exact max; a strip that misses it is redone with
+//   the exact max, and its offsets move for the next window.  fp32
+//   (attend_f32) keeps an online softmax over key chunks.
 //
 // Padding
 //   Keys are padded to NP = 16*NT: padded key columns get a -inf bias
@@ -60,12 +61,16 @@
 //   and Q rows past N are copies of row N-1 in LDS (zero on the register
 //   path), harmless under those biases.  The kernel needs no workspace.
 //
-// Numerics follow torch-ext/crumpet/fused_attention.py:82-146: q is scaled
-// in fp32 and rounded back to the input type, products accumulate in fp32,
-// bias and mask are added in fp32, P is rounded (RNE) to the input type
-// before the second product, and the output is acc / rowsum rounded to the
-// output type.  The row sum is taken over the rounded P (the same values the
-// numerator uses).
+// Numerics follow torch-ext/crumpet/fused_attention.py:82-146: products
+// accumulate in fp32, bias and mask are added in fp32, P is rounded (RNE) to
+// the input type before the second product, and the output is acc / rowsum
+// rounded to the output type.  The reference rounds q * scale to the input
+// type; here q * scale * log2(e) enters as hi + lo, which carries it to
+// about twice the input precision (for the default scale 16^-0.5 the
+// reference's q * scale is exact, and so is this to within fp32).  The row
+// sum is taken over the rounded P (the same values the numerator uses; the
+// reference sums the unrounded fp32 P): both stay within the tolerance of
+// the fp32 formula, and the difference is at most one rounding of P per key.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -220,17 +225,48 @@ __device__ __forceinline__ typename Frag<T>::x4 scaled(typename Frag<T>::x4 v, f
     return v;
 }
 
+// Four dims of a Q row into LDS at row + d0.  2-byte types store
+// hi = q * scale rounded (scale includes log2(e)) at d0 and the remainder
+// lo = q * scale - hi, rounded, at 16 + d0: hi + lo carries q * scale to
+// about twice the input precision, so folding log2(e) into the operand adds
+// no rounding of its own.  fp32 stores q * scale.
+template <typename T>
+__device__ __forceinline__ void store_q4(T* row, int d0, typename Frag<T>::x4 v, float scale) {
+    typedef typename Frag<T>::x4 X4;
+    if constexpr (sizeof(T) == 2) {
+        X4 hi, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float x = static_cast<float>(v[e]) * scale;
+            hi[e] = T(x);
+            lo[e] = T(x - static_cast<float>(hi[e]));
+        }
+        *reinterpret_cast<X4*>(row + d0) = hi;
+        *reinterpret_cast<X4*>(row + 16 + d0) = lo;
+    } else {
+        *reinterpret_cast<X4*>(row + d0) = scaled<T>(v, scale);
+    }
+}
+
 // K layout in LDS.  2-byte types: each 16-row key tile stores the first 8
-// dims of its 16 rows (16 B each), then the last 8, so the 32 lanes of a
-// half-wave that read one key fragment (rows 0-15, dims 4g..4g+3, g = 0, 1)
-// cover 256 contiguous bytes; with plain 32-byte rows they would cover only
-// half of each row and collide on the banks.  fp32: plain rows.
+// dims of its 16 rows (16 B each), then the last 8, so the lanes 0-31 that
+// read one 16x16x32 key fragment (row col, dims 8g..8g+7, g = 0, 1) cover
+// 512 contiguous bytes (lanes 32-63 read the same bytes again: the score
+// product repeats K in its dims 16-31, attend_offset).  fp32: plain rows.
 template <typename T>
 __device__ __forceinline__ constexpr int kidx(int row, int d) {
     if constexpr (sizeof(T) == 2)
         return (row >> 4) * 256 + (d >> 3) * 128 + (row & 15) * 8 + (d & 7);
     else
         return row * 16 + d;
+}
+
+// Q layout in LDS: 2-byte types keep 32 elements per row, the rounded
+// q * scale * log2(e) (dims 0-15) and the rounding remainder (dims 16-31);
+// fp32 keeps the 16 dims of q * scale.
+template <typename T>
+constexpr int q_row_elems() {
+    return sizeof(T) == 2 ? 32 : 16;
 }
 
 template <typename T>
@@ -248,8 +284,8 @@ __device__ __forceinline__ typename Frag<T>::x4 zero4() {
 // loop gains more from the third wave than it loses to the smaller budget.
 template <typename T, int NT, int kMask, bool kVec>
 constexpr int waves_per_eu() {
-    // (an fp32 mask's prefetch ring needs a few more registers than 168 at
-    // 22 tiles)
+    // (an fp32 mask's prefetch needs a few more registers than 168 at 22
+    // tiles)
     if constexpr (sizeof(T) == 2 && kVec && !(kMask == kMaskF32 && NT > 14))
         return NT <= 4 ? 4 : (NT <= 22 ? 3 : 2);
     return NT <= 4 ? 4 : (NT <= 8 ? 3 : 2);
@@ -354,6 +390,19 @@ __device__ __forceinline__ typename Frag<T>::x4 lds_read_tr(const T* ptr) {
     return __builtin_bit_cast(typename Frag<T>::x4, r);
 }
 
+// Byte address of an LDS object, and a load of V from such an address
+// (keeps the LDS address space where a pointer has to be made opaque).
+template <typename T>
+__device__ __forceinline__ uint32_t lds_byte_addr(const T* ptr) {
+    typedef const __attribute__((address_space(3))) T LdsT;
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)ptr));
+}
+template <typename V>
+__device__ __forceinline__ V lds_load(uint32_t addr) {
+    typedef const __attribute__((address_space(3))) V LdsV;
+    return *reinterpret_cast<LdsV*>(static_cast<uintptr_t>(addr));
+}
+
 // Staging of one window's Q (this group's rows), K and V into LDS.  Each
 // thread owns chunks c = tid + k * kThreads of 4 elements; kQChunks Q chunks
 // come first, then NP*4 K chunks, then NP*4 V chunks.
@@ -399,7 +448,7 @@ struct Stage {
         for (int k = 0; k < kPerThread; ++k) {
             const int c = threadIdx.x + k * kThreads;
             if (c < kQChunks) {
-                *reinterpret_cast<X4*>(&q_lds[c * 4]) = scaled<T>(r[k], scale);
+                store_q4<T>(&q_lds[(c >> 2) * q_row_elems<T>()], (c & 3) * 4, r[k], scale);
             } else if (c < kChunks) {
                 const int cc = c - kQChunks;
                 if (cc < NP * 4) {
@@ -427,6 +476,8 @@ struct Stage {
 // rows meet P = 0 and padded query rows are never stored.  No branches and
 // no 64-bit address arithmetic per row.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 // Buffer descriptor words (base, stride 0, num_records, dword-3 flags) for a
 // window's rows, workgroup-uniform.
@@ -537,7 +588,7 @@ struct Stage<T, NT, true> {
     __device__ __forceinline__ void store(float scale, T* q_lds, T* k_lds, T* vt_lds) const {
         const int tid = threadIdx.x;
         const int n0 = tid >> 2, d0 = (tid & 3) * 4;
-        *reinterpret_cast<X4*>(&q_lds[tid * 4]) = scaled<T>(rq, scale);
+        store_q4<T>(&q_lds[n0 * q_row_elems<T>()], d0, rq, scale);
         if constexpr (!kDma) {
 #pragma unroll
             for (int k = 0; k < kKC; ++k) {
@@ -561,10 +612,12 @@ struct Stage<T, NT, true> {
 // rows get 0 (never stored).  In region mode a key whose shift-region class
 // differs from the query's on an axis that the window type `code` splits
 // gets -100.  Runs when the window type changes (at most 8 times per
-// workgroup), never per window.
-template <int NT, int kMask>
+// workgroup), never per window.  kLog2: the tiles are kept in log2 units
+// (multiplied by log2(e)) plus the query's row offset `off`, for the offset
+// softmax of the 2-byte types (attend_offset).
+template <int NT, int kMask, bool kLog2>
 __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, int h, int qi, int g,
-                                            int code, const uint8_t* cls) {
+                                            int code, const uint8_t* cls, float off) {
     // Re-read the kernel arguments (Params is the kernel's only argument, at
     // offset 0 of the kernarg segment) through an opaque copy of the segment
     // pointer, so that the compiler loads them here instead of keeping them
@@ -617,6 +670,7 @@ __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, 
             if constexpr (kMask == kMaskRegion) {
                 if ((split >> (8 * r)) & 0xffu) val += -100.0f;
             }
+            if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
             val = row ? val : 0.0f;
             bs[t][r] = (16 * t + 4 * g + r) < N ? val : -INFINITY;
         }
@@ -636,31 +690,340 @@ __device__ __forceinline__ float xmax32(float m) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// One strip (16 queries, NT*16 keys) of one window.
+// ---------------------------------------------------------------------------
+// Offset softmax (2-byte types)
+//
+// Scores come out of the score product in log2 units, so that P = 2^S needs
+// no multiply-add: the bias (+ region mask) tiles are kept multiplied by
+// log2(e), and Q by scale * log2(e).  Q enters the 16x16x32 product as
+// hi + lo (store_q4): dims 0-15 carry K . Q_hi, dims 16-31 (K repeated)
+// K . Q_lo, so the folded log2(e) adds no rounding beyond fp32.
+//
+// No row max is taken.  The bias tiles carry a per-query offset instead
+// (build_tiles), and softmax is invariant to it, so the offset only has to
+// keep P inside the range where rounding to the input type costs no more
+// than with the exact max: every P below 2^15 (finite in fp16) and a row
+// sum of at least 1 (the probabilities that carry weight are normal
+// numbers).  The row sums come out of the same pass (ones^T P^T), so the
+// check is exact: when a strip's row sums miss [1, 2^15) (a bad first
+// guess, or scores that moved from earlier windows), the wave redoes the
+// strip with the exact row max subtracted in the fp32 accumulator, as the
+// reference does, and moves its offsets so that a window like this one
+// would have row sums near 2^kOffsetTarget; the caller rebuilds the wave's
+// bias tiles with them before its next window (the tiles stay read-only
+// here, which keeps them in registers).
+//
+// Per score this leaves one exp and half a conversion on the VALU; with no
+// max reduction between the score tiles, pair p+1's score MFMAs are issued
+// next to pair p's exps, and K, V and mask fragments are requested one or
+// two pairs ahead.
+constexpr float kOffsetTarget = 7.0f;     // log2 of the row sum aimed at
+constexpr float kRowSumLimit = 32768.0f;  // row sums (hence every P) stay below 2^15
+
 template <typename T, int NT, int kMask, bool kUseMask, bool kVec>
-__device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
-                                       const T* __restrict__ k_lds, const T* __restrict__ vt_lds,
-                                       int b, int h, int wave, int qi, int col, int g) {
+__device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
+                                              const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
+                                              int h, int wave, int qi, int col, int g, float& off) {
     typedef typename Frag<T>::x4 X4;
-    constexpr int kVtStride = Stage<T, NT, kVec>::kVtStride;
+    typedef typename Frag<T>::x8 X8;
     constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
+    constexpr int kPairs = (NT + 1) / 2;
+    const int N = p.N;
+
+    // Q^T operand of S^T = K Q^T (16x16x32): lane (col, g) holds elements
+    // 8g..8g+7 of query col's LDS row, i.e. Q_hi dims for g < 2 and Q_lo
+    // dims for g >= 2.
+    const X8 qf = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * 32 + 8 * g]);
+
+    // K operand: lane (col, g) reads row col of the tile, dims 8(g&1)..+7
+    const T* kbase = k_lds + (g & 1) * 128 + col * 8;
+    auto kfrag = [&](int t) -> X8 { return *reinterpret_cast<const X8*>(kbase + t * 256); };
+    // V^T fragments by transpose reads of row-major V (lds_read_tr)
+    const T* vrow = &v_lds[(4 * g + (col >> 2)) * 16 + (col & 3) * 4];
+
+    // Tensor mask through a buffer descriptor spanning exactly the window's
+    // [N, N] extent (see attend_f32 for the padding and end-of-extent rules).
+    __amdgpu_buffer_rsrc_t mrsrc;
+    int mvoff = 0;
+    if constexpr (kUseMask) {
+        const int qr = qi < N ? qi : N - 1;
+        char* mb = uniform_ptr(static_cast<const char*>(p.mask) +
+                               int64_t(b % p.mask_batch) * p.ms[0] * kMaskBytes);
+        const int extent =
+            __builtin_amdgcn_readfirstlane(static_cast<int>(((N - 1) * p.ms[1] + N) * kMaskBytes));
+        mrsrc = __builtin_amdgcn_make_buffer_rsrc(mb, 0, extent, 0x00020000);
+        mvoff = static_cast<int>((qr * p.ms[1] + 4 * g) * kMaskBytes);
+    }
+    // 2-byte masks: a row of an odd row stride starts in the middle of a
+    // dword, and unaligned 8-byte loads are slow.  Each lane therefore loads
+    // the three dwords around its 4 keys from a dword-aligned offset and
+    // shifts its halves into place when it uses them (mshift: 0 or 16 bits).
+    // The words held per tile: 3 (2-byte) or 4 (fp32).
+    int mshift = 0;
+    if constexpr (kUseMask && kMaskBytes == 2) {
+        mshift = (mvoff & 2) * 8;
+        mvoff &= ~3;
+    }
+    constexpr int kMWords = kMaskBytes == 2 ? 3 : 4;
+    typedef uint32_t MaskWords[kMWords];
+    auto fetch = [&](int t, MaskWords& w) {
+        if constexpr (kUseMask) {
+            const int o = mvoff + 16 * t * kMaskBytes;
+            if constexpr (kMaskBytes == 2) {
+                const u32x3 v3 = __builtin_amdgcn_raw_buffer_load_b96(mrsrc, o, 0, 0);
+                w[0] = v3[0];
+                w[1] = v3[1];
+                w[2] = v3[2];
+            } else {
+                const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) w[r] = v4[r];
+            }
+            if (t == NT - 1 && qi == N - 1 && 16 * t + 4 * g + 3 >= N) {
+                // this load reaches past the extent end, where a range check
+                // at dword granularity could zero in-range keys: read the 4
+                // keys element by element and lay them out as the three
+                // dwords would hold them
+                if constexpr (kMaskBytes == 2) {
+                    uint32_t kv[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        kv[r] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, o + mshift / 8 + 2 * r, 0, 0);
+                    if (mshift != 0) {
+                        w[0] = kv[0] << 16;
+                        w[1] = kv[1] | (kv[2] << 16);
+                        w[2] = kv[3];
+                    } else {
+                        w[0] = kv[0] | (kv[1] << 16);
+                        w[1] = kv[2] | (kv[3] << 16);
+                        w[2] = 0u;
+                    }
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, o + 4 * r, 0, 0);
+                }
+            }
+        }
+    };
+    // accumulator input of tile t: bias (+ region mask) tile with the row
+    // offset, plus the mask tensor's values in log2 units
+    auto cinit = [&](int t, const MaskWords& w) -> f32x4 {
+        f32x4 c = bs[t];
+        if constexpr (kUseMask) {
+            uint32_t hw[2] = {0u, 0u};  // 2-byte masks: the 4 keys' halves in place
+            if constexpr (kMaskBytes == 2) {
+                hw[0] = __builtin_amdgcn_alignbit(w[1], w[0], mshift);
+                hw[1] = __builtin_amdgcn_alignbit(w[2], w[1], mshift);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float mv;
+                if constexpr (kMask == kMaskF32)
+                    mv = __uint_as_float(w[r]);
+                else if constexpr (kMask == kMaskF16)
+                    mv = static_cast<float>(
+                        __builtin_bit_cast(_Float16, static_cast<uint16_t>(r & 1 ? hw[r >> 1] >> 16 : hw[r >> 1])));
+                else
+                    mv = __uint_as_float(r & 1 ? (hw[r >> 1] & 0xffff0000u) : (hw[r >> 1] << 16));
+                c[r] = __builtin_fmaf(mv, kLog2e, c[r]);
+            }
+        }
+        return c;
+    };
+
+    X8 ones8;
+#pragma unroll
+    for (int r = 0; r < 8; ++r) ones8[r] = T(1.0f);
+
+    // P of the pair of tiles (t, t + 1), rounded to T: B operand of the
+    // product below
+    auto probs = [&](const f32x4& s0, const f32x4& s1, bool has1) -> X8 {
+        X8 pb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pb[r] = T(__builtin_amdgcn_exp2f(s0[r]));
+            pb[r + 4] = has1 ? T(__builtin_amdgcn_exp2f(s1[r])) : T(0.0f);
+        }
+        return pb;
+    };
+    // O^T += V^T P^T and the row sums (ones^T P^T) for the pair
+    auto accumulate = [&](const X8& pb, const X4& v0, const X4& v1, bool has1, f32x4& o, f32x4& lacc) {
+        X8 va;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            va[r] = v0[r];
+            va[r + 4] = has1 ? v1[r] : T(0.0f);
+        }
+        o = Frag<T>::mma32(va, pb, o);
+        lacc = Frag<T>::mma32(ones8, pb, lacc);
+    };
+
+    f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
+    {
+        // Software pipeline over tile pairs.  Iteration pr requests the V
+        // fragments of pair pr, the K fragments of pair pr + kKAhead and the
+        // mask words of pair pr + kMaskAhead, issues the score MFMAs of pair
+        // pr+1, and exponentiates pair pr and multiplies it into O (its V
+        // reads are covered by the exps).  K is requested two pairs ahead
+        // and pair pr+1's score MFMAs run during pair pr's exps, except with
+        // a mask tensor at 3 waves per SIMD: there the mask words and the
+        // accumulator inputs take the registers of the second K pair, so K
+        // is requested one pair ahead and the score MFMAs follow the exps
+        // that cover its LDS latency.  All indices are compile-time
+        // constants, so the arrays live in registers.
+        // register budget above 168 left after the bias tiles (not at 32 tiles)
+        constexpr bool kWide = waves_per_eu<T, NT, kMask, kVec>() < 3 && NT <= 22;
+        constexpr int kKAhead = (kUseMask && !kWide) ? 1 : 2;
+        constexpr int kMaskAhead = kWide ? 2 : 1;  // pairs
+        X8 kf[NT];
+        f32x4 S[NT];
+        MaskWords mw[kUseMask ? NT : 1];
+#pragma unroll
+        for (int t = 0; t < NT && t < 2 * kKAhead; ++t) kf[t] = kfrag(t);
+        if constexpr (kUseMask) {
+#pragma unroll
+            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t) fetch(t, mw[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < NT && t < 2; ++t) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
+#pragma unroll
+        for (int pr = 0; pr < kPairs; ++pr) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int t0 = 2 * pr;
+            const bool has1 = t0 + 1 < NT;
+            const X4 v0 = lds_read_tr<T>(vrow + 256 * t0);
+            const X4 v1 = has1 ? lds_read_tr<T>(vrow + 256 * (t0 + 1)) : v0;
+#pragma unroll
+            for (int t = t0 + 2 * kKAhead; t < t0 + 2 * kKAhead + 2; ++t)
+                if (t < NT) kf[t] = kfrag(t);
+            if constexpr (kUseMask) {
+#pragma unroll
+                for (int t = t0 + 2 * kMaskAhead; t < t0 + 2 * kMaskAhead + 2; ++t)
+                    if (t < NT) fetch(t, mw[t]);
+            }
+            X8 pb;
+            if constexpr (kKAhead == 1) {
+                pb = probs(S[t0], S[has1 ? t0 + 1 : t0], has1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+#pragma unroll
+            for (int t = t0 + 2; t < t0 + 4; ++t)
+                if (t < NT) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
+            if constexpr (kKAhead != 1) pb = probs(S[t0], S[has1 ? t0 + 1 : t0], has1);
+            accumulate(pb, v0, v1, has1, o, lacc);
+            asm volatile("" : "+v"(o));  // as in the exact pass below
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    float l = lacc[0];  // every row of ones^T P^T holds the sum of query col
+    const bool bad = qi < N && !(l >= 1.0f && l < kRowSumLimit);
+    bool exact = false;  // the exact pass ran and moved the offsets (wave-uniform)
+    if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+        // Exact pass: the row max of the scores, then the strip again with
+        // the max subtracted in the fp32 accumulator.  Each pass reads K
+        // (and the mask) through opaque copies of the fragment bases, so
+        // that the compiler reads them again instead of keeping an earlier
+        // pass's fragments live across the passes.
+        uint32_t ka = lds_byte_addr(kbase);
+        int mva = mvoff;
+        asm volatile("" : "+v"(ka), "+v"(mva));
+        mvoff = mva;
+        float m0 = -INFINITY, m1 = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            __builtin_amdgcn_sched_barrier(0);
+            MaskWords w;
+            fetch(t, w);
+            const f32x4 sc = Frag<T>::mma32(lds_load<X8>(ka + t * 512), qf, cinit(t, w));
+            m0 = fmaxf(fmaxf(m0, sc[0]), sc[1]);
+            m1 = fmaxf(fmaxf(m1, sc[2]), sc[3]);
+            // keeps each tile's max here (pure math may otherwise be sunk
+            // below the loop, keeping every score tile live)
+            asm volatile("" : "+v"(m0), "+v"(m1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const float m = xmax32(xmax16(fmaxf(m0, m1)));
+        o = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        lacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t kb = lds_byte_addr(kbase);
+        int mvb = mvoff;
+        asm volatile("" : "+v"(kb), "+v"(mvb));
+        mvoff = mvb;
+#pragma unroll
+        for (int pr = 0; pr < kPairs; ++pr) {
+            __builtin_amdgcn_sched_barrier(0);
+            const int t0 = 2 * pr;
+            const bool has1 = t0 + 1 < NT;
+            MaskWords w0, w1;
+            fetch(t0, w0);
+            if (has1) fetch(t0 + 1, w1);
+            const f32x4 s0 = Frag<T>::mma32(lds_load<X8>(kb + t0 * 512), qf, cinit(t0, w0) - m);
+            f32x4 s1 = s0;
+            if (has1) s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * 512), qf, cinit(t0 + 1, w1) - m);
+            const X4 v0 = lds_read_tr<T>(vrow + 256 * t0);
+            const X4 v1 = has1 ? lds_read_tr<T>(vrow + 256 * (t0 + 1)) : v0;
+            accumulate(probs(s0, s1, has1), v0, v1, has1, o, lacc);
+            // keeps the O product in this iteration (it would otherwise be
+            // sunk towards the store, keeping every V fragment live)
+            asm volatile("" : "+v"(o));
+        }
+        l = lacc[0];
+        // move the offsets: a window like this one would have row sums
+        // near 2^kOffsetTarget (rows whose scores are not finite keep theirs)
+        const float delta = kOffsetTarget - m - __builtin_amdgcn_logf(l);
+        off += (delta - delta == 0.0f) ? delta : 0.0f;  // 0 for NaN and infinities
+        exact = true;
+    }
+
+    // lane holds O[qi][4g + r], r = 0..3
+    if (qi < N) {
+        T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
+        const float inv = 1.0f / l;
+        X4 res;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) res[r] = T(o[r] * inv);
+        if constexpr (kVec) {
+            *reinterpret_cast<X4*>(orow + 4 * g) = res;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) orow[(4 * g + r) * p.os[3]] = res[r];
+        }
+    }
+    return exact;
+}
+
+// One strip (16 queries, NT*16 keys) of one window, fp32 operands: the
+// scores run on v_mfma_f32_16x16x4f32 (four steps over the head dim) and
+// the softmax is online over key chunks of at most 6 tiles with a lazy
+// rescale: the first chunk sets the row max exactly; a later chunk
+// exponentiates against the running max unless one of its scores exceeds it
+// by more than kLazyMargin (a wave-uniform test), in which case the max is
+// refreshed across the lane groups and O and the row sum are rescaled
+// first.  The row sum is taken on the VALU.
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec>
+__device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
+                                           const T* __restrict__ k_lds, const T* __restrict__ vt_lds, int b,
+                                           int h, int wave, int qi, int col, int g) {
+    static_assert(sizeof(T) == 4, "2-byte types run attend_offset");
+    constexpr int kVtStride = Stage<T, NT, kVec>::kVtStride;
     constexpr int kPrefetch = NT < 6 ? NT : 6;
     const int N = p.N;
 
     // B operand of S^T = K Q^T: Q[qi][4g..4g+3] (pre-scaled in LDS)
-    const X4 qf = *reinterpret_cast<const X4*>(&q_lds[(wave * 16 + col) * 16 + 4 * g]);
+    const f32x4 qf = *reinterpret_cast<const f32x4*>(&q_lds[(wave * 16 + col) * 16 + 4 * g]);
 
     // Tensor mask through a buffer descriptor spanning exactly the window's
     // [N, N] extent: offsets past it return 0, so no per-key test is needed;
     // padded keys read a finite neighbour (their bias is -inf) and padded
     // query rows read row N-1 (never stored).  A lane's 4 keys of a tile are
-    // contiguous in the mask row, so each tile is one 8-byte (16-bit masks)
-    // or 16-byte (fp32 masks) load; the target accesses memory unaligned, so
-    // an odd row stride is fine.  Only the last tile of row N-1 can reach
-    // past the extent, and a range check at dword or access granularity
-    // would then zero in-range keys sharing the load, so those lanes read
-    // that tile again element by element.  Offsets are immediates.
-    typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+    // contiguous in the mask row: one 8-byte (16-bit masks) or 16-byte (fp32
+    // masks) load per tile.  Only the last tile of row N-1 can reach past
+    // the extent, and a range check at dword or access granularity would
+    // then zero in-range keys sharing the load, so those lanes read that
+    // tile again element by element.  Offsets are immediates.
+    constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
     constexpr int kMaskWords = kMaskBytes;  // 32-bit words per lane and tile
     __amdgpu_buffer_rsrc_t mrsrc;
     int mvoff = 0;
@@ -679,7 +1042,7 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
         if constexpr (kUseMask) {
             const int off = mvoff + 16 * t * kMaskBytes;
             if constexpr (kMaskBytes == 2) {
-                const u32x2v w = __builtin_amdgcn_raw_buffer_load_b64(mrsrc, off, 0, 0);
+                const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(mrsrc, off, 0, 0);
                 mq[2 * slot] = w[0];
                 mq[2 * slot + 1] = w[1];
             } else {
@@ -693,11 +1056,11 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if constexpr (kMaskBytes == 2) {
-                        const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off + 2 * r, 0, 0);
+                        const uint32_t hv = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, off + 2 * r, 0, 0);
                         if (r & 1)
-                            mq[2 * slot + (r >> 1)] |= h << 16;
+                            mq[2 * slot + (r >> 1)] |= hv << 16;
                         else
-                            mq[2 * slot + (r >> 1)] = h;
+                            mq[2 * slot + (r >> 1)] = hv;
                     } else {
                         mq[4 * slot + r] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, off + 4 * r, 0, 0);
                     }
@@ -710,33 +1073,18 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
         for (int t = 0; t < kPrefetch; ++t) fetch(t, t);
     }
 
-    // Keys are processed in chunks of at most 6 tiles with an online softmax
-    // between chunks, which keeps only one chunk of scores in registers next
-    // to the bias tiles.  The first chunk sets the row max exactly; a later
-    // chunk exponentiates against the running max unless one of its scores
-    // exceeds it by more than kLazyMargin (a wave-uniform test), in which
-    // case the max is refreshed across the lane groups and O and the row
-    // sums are rescaled first.  Softmax is invariant to the offset, so only
-    // the rare refresh costs a cross-lane reduction.
     constexpr int kNumChunks = (NT + 5) / 6;
     constexpr int kChunk = (NT + kNumChunks - 1) / kNumChunks;
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-    f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
-    float lsum = 0.0f;  // fp32 path row sum (VALU)
+    float lsum = 0.0f;
     float m_run = -INFINITY;
     float mb_run = 0.0f;  // m_run * log2(e)
-    // V^T fragments: transposed layout (fp32) or transpose reads of row-major V
-    const T* vrow = v_row_major<T>() ? &vt_lds[(4 * g + (col >> 2)) * 16 + (col & 3) * 4]
-                                     : &vt_lds[col * kVtStride + 4 * g];
+    const T* vrow = &vt_lds[col * kVtStride + 4 * g];  // transposed V
 
 #pragma unroll
     for (int c0 = 0; c0 < NT; c0 += kChunk) {
         // chunks must not interleave: that would keep two chunks of scores live
         __builtin_amdgcn_sched_barrier(0);
-        // matrix sections run at raised wave priority, the softmax at the
-        // normal one, so that a SIMD's waves tend to alternate between the
-        // two pipes (1-2%)
-        __builtin_amdgcn_s_setprio(1);
         const int cn = (NT - c0 < kChunk) ? NT - c0 : kChunk;
         f32x4 S[kChunk];
 #pragma unroll
@@ -761,21 +1109,14 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
                 }
                 if (t + kPrefetch < NT) fetch(t + kPrefetch, slot);
             }
-            if constexpr (sizeof(T) == 2) {
-                const X4 kf = *reinterpret_cast<const X4*>(&k_lds[kidx<T>(16 * t + col, 4 * g)]);
-                S[u] = Frag<T>::mma16(kf, qf, c);
-            } else {
-                const f32x4 kf = *reinterpret_cast<const f32x4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
-                f32x4 acc = c;
+            const f32x4 kf = *reinterpret_cast<const f32x4*>(&k_lds[(16 * t + col) * 16 + 4 * g]);
+            f32x4 acc = c;
 #pragma unroll
-                for (int kk = 0; kk < 4; ++kk)
-                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kk], qf[kk], acc, 0, 0, 0);
-                S[u] = acc;
-            }
+            for (int kk = 0; kk < 4; ++kk) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[kk], qf[kk], acc, 0, 0, 0);
+            S[u] = acc;
             if constexpr (kUseMask) __builtin_amdgcn_sched_barrier(0);  // keep the mask ring
         }
 
-        __builtin_amdgcn_s_setprio(0);
         // lane-local chunk max: two 3-input maxes per tile on two chains
         float m0 = m_run, m1 = -INFINITY;
 #pragma unroll
@@ -798,91 +1139,41 @@ __device__ __forceinline__ void attend(const Params& p, const f32x4 (&bs)[NT], c
             const float mbn = m * kLog2e;
             const float alpha = __builtin_amdgcn_exp2f(mb_run - mbn);
             o *= alpha;
-            lacc *= alpha;
             lsum *= alpha;
             m_run = m;
             mb_run = mbn;
         }
         const float mb = mb_run;
-
 #pragma unroll
         for (int u = 0; u < kChunk; ++u) {
             if (u >= cn) break;
 #pragma unroll
             for (int r = 0; r < 4; ++r) S[u][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(S[u][r], kLog2e, -mb));
         }
-
-        __builtin_amdgcn_s_setprio(1);
-        // O^T += V^T P^T; the row sums ride on the matrix pipe as ones^T P^T
-        if constexpr (sizeof(T) == 2) {
-            typedef typename Frag<T>::x8 X8;
-            X8 ones8;
+        // O^T += V^T P^T
 #pragma unroll
-            for (int r = 0; r < 8; ++r) ones8[r] = T(1.0f);
+        for (int u = 0; u < kChunk; ++u) {
+            if (u >= cn) break;
+            const f32x4 v0 = *reinterpret_cast<const f32x4*>(vrow + 16 * (c0 + u));
 #pragma unroll
-            for (int u = 0; u + 1 < kChunk; u += 2) {
-                if (u + 1 >= cn) break;
-                const int t = c0 + u;
-                X8 pb, va;
-                const X4 v0 = lds_read_tr<T>(vrow + 256 * t);
-                const X4 v1 = lds_read_tr<T>(vrow + 256 * (t + 1));
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pb[r] = T(S[u][r]);
-                    pb[r + 4] = T(S[u + 1][r]);
-                    va[r] = v0[r];
-                    va[r + 4] = v1[r];
-                }
-                o = Frag<T>::mma32(va, pb, o);
-                lacc = Frag<T>::mma32(ones8, pb, lacc);
-            }
-            if (cn & 1) {
-                // odd tile: the same 16x16x32 instruction with a zero upper
-                // half, so each accumulator chain uses a single MFMA opcode
-                const int u = cn - 1;
-                X8 pb, va;
-                const X4 v0 = lds_read_tr<T>(vrow + 256 * (c0 + u));
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    pb[r] = T(S[u][r]);
-                    pb[r + 4] = T(0.0f);
-                    va[r] = v0[r];
-                    va[r + 4] = T(0.0f);
-                }
-                o = Frag<T>::mma32(va, pb, o);
-                lacc = Frag<T>::mma32(ones8, pb, lacc);
-            }
-        } else {
-#pragma unroll
-            for (int u = 0; u < kChunk; ++u) {
-                if (u >= cn) break;
-                const f32x4 v0 = *reinterpret_cast<const f32x4*>(vrow + 16 * (c0 + u));
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    o = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[r], S[u][r], o, 0, 0, 0);
-                    lsum += S[u][r];
-                }
+            for (int r = 0; r < 4; ++r) {
+                o = __builtin_amdgcn_mfma_f32_16x16x4f32(v0[r], S[u][r], o, 0, 0, 0);
+                lsum += S[u][r];
             }
         }
     }
-    __builtin_amdgcn_s_setprio(0);
-    float l;
-    if constexpr (sizeof(T) == 2) {
-        l = lacc[0];  // every row of ones^T P^T holds the sum for query col
-    } else {
-        lsum += __shfl_xor(lsum, 16);
-        l = lsum + __shfl_xor(lsum, 32);
-    }
+    lsum += __shfl_xor(lsum, 16);
+    const float l = lsum + __shfl_xor(lsum, 32);
 
     // lane holds O[qi][4g + r], r = 0..3
     if (qi < N) {
         T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
         const float inv = 1.0f / l;
-        X4 res;
+        f32x4 res;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) res[r] = T(o[r] * inv);
+        for (int r = 0; r < 4; ++r) res[r] = o[r] * inv;
         if constexpr (kVec) {
-            *reinterpret_cast<X4*>(orow + 4 * g) = res;
+            *reinterpret_cast<f32x4*>(orow + 4 * g) = res;
         } else {
 #pragma unroll
             for (int r = 0; r < 4; ++r) orow[(4 * g + r) * p.os[3]] = res[r];
@@ -896,7 +1187,7 @@ __attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask, kVec>(), waves_per
 swin_attention_d16_kernel(const Params p) {
     typedef Stage<T, NT, kVec> St;
     constexpr int NP = St::NP;
-    __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * 16];
+    __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * q_row_elems<T>()];
     __shared__ __attribute__((aligned(16))) T k_lds[2][St::kRows * 16];
     __shared__ __attribute__((aligned(16))) T vt_lds[2][St::kVLds];
     __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
@@ -944,6 +1235,10 @@ swin_attention_d16_kernel(const Params p) {
         }
     }
 
+    // 2-byte types: scores in log2 units (attend_offset), so Q carries log2(e)
+    const float qscale = sizeof(T) == 2 ? p.scale * kLog2e : p.scale;
+    float off = 0.0f;  // row offset of the offset softmax (2-byte types, log2 units)
+
     St st;
     WindowIter<kMask> it;
     it.init(p, i0);
@@ -952,6 +1247,7 @@ swin_attention_d16_kernel(const Params p) {
         it.stride = p.ranges;
     }
     int code_cur = -1;
+    bool rebuild = false;  // this wave's offsets moved: rebuild its tiles (wave-uniform)
     int code_next;
     int b_next = it.window(p, code_next);
     // tensor mode: the window's boundary flag is read before the next
@@ -960,7 +1256,7 @@ swin_attention_d16_kernel(const Params p) {
     if constexpr (kMask != kNoMask && kMask != kMaskRegion)
         flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
     st.load(p, b_next, h, q0, k_lds[0], vt_lds[0]);
-    st.store(p.scale, q_lds[0], k_lds[0], vt_lds[0]);
+    st.store(qscale, q_lds[0], k_lds[0], vt_lds[0]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
     __syncthreads();
 
@@ -974,9 +1270,10 @@ swin_attention_d16_kernel(const Params p) {
         // rows are requested: the vector-memory counter retires in order, so
         // waiting for the bias loads after that request would wait for the
         // rows as well.
-        if (active && code != code_cur) {  // code is workgroup-uniform
-            build_tiles<NT, kMask>(bs, p, h, qi, g, code, cls_lds);
+        if (active && (code != code_cur || rebuild)) {  // code is workgroup-uniform
+            build_tiles<NT, kMask, sizeof(T) == 2>(bs, p, h, qi, g, code, cls_lds, off);
             code_cur = code;
+            rebuild = false;
         }
         if (i + 1 < i1) {
             it.next(p);
@@ -986,16 +1283,26 @@ swin_attention_d16_kernel(const Params p) {
             st.load(p, b_next, h, q0, k_lds[buf ^ 1], vt_lds[buf ^ 1]);
         }
         if (active) {
+            constexpr bool kTensor = kMask != kNoMask && kMask != kMaskRegion;
             bool use_mask = false;
-            if constexpr (kMask != kNoMask && kMask != kMaskRegion) use_mask = flag;
-            if (use_mask)
-                attend<T, NT, kMask, (kMask != kNoMask && kMask != kMaskRegion), kVec>(
-                    p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h, wave, qi, col, g);
-            else
-                attend<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b,
-                                                  h, wave, qi, col, g);
+            if constexpr (kTensor) use_mask = flag;
+            if constexpr (sizeof(T) == 2) {
+                if (use_mask)
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec>(p, bs, q_lds[buf], k_lds[buf],
+                                                                         vt_lds[buf], b, h, wave, qi, col, g, off);
+                else
+                    rebuild = attend_offset<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf],
+                                                                       vt_lds[buf], b, h, wave, qi, col, g, off);
+            } else {
+                if (use_mask)
+                    attend_f32<T, NT, kMask, kTensor, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h,
+                                                            wave, qi, col, g);
+                else
+                    attend_f32<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h,
+                                                          wave, qi, col, g);
+            }
         }
-        if (i + 1 < i1) st.store(p.scale, q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+        if (i + 1 < i1) st.store(qscale, q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
         __syncthreads();
     }

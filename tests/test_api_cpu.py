@@ -63,13 +63,17 @@ def test_no_cpu_fallback():
         crumpet_amd.compute_attn_mask_3d(14, 14, 14, (7, 7, 7), (3, 3, 3), torch.float16, "cpu")
 
 
-def test_missing_extension_raises(monkeypatch):
+def test_missing_extension_raises(monkeypatch, tmp_path):
+    """With the libraries absent the loader reports it (and tries again on
+    the next call, so a build in the same process is picked up)."""
     from crumpet_amd import _native
 
     monkeypatch.setattr(_native, "_ops", None)
-    monkeypatch.setattr(_native, "_error", "OSError: not built")
+    monkeypatch.setattr(_native, "_error", None)
+    monkeypatch.setattr(_native, "HIP_LIB", tmp_path / "libcrumpet_hip.so")
     with pytest.raises(RuntimeError, match="not available"):
         _native.ops()
+    assert "not built" in _native.load_error()
 
 
 def test_cache_hit_and_miss():
