@@ -26,91 +26,47 @@ from typing import Sequence
 import torch
 
 from . import _native
+from ._geometry import WindowGrid, as_triple, require_float_dtype
 from .cache import clear_mask_cache, get_or_compute_mask, make_mask_key, mask_cache_info
 
 __version__ = "0.1.0"
 
-_ops = _native.ops_or_none()
-_HAS_HIP_EXT = _ops is not None
-
-_SUPPORTED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+_HAS_HIP_EXT = _native.ops_or_none() is not None
 
 
-def _register_fake_impls() -> None:
-    """No-op fake kernels so the mutating ops trace under torch.compile / FakeTensor."""
-    if not _HAS_HIP_EXT:
-        return
-    register = getattr(torch.library, "register_fake", None)
-    if register is None:
-        return
+class _RoctxRange:
+    """A roctx range (``torch.cuda.nvtx`` is roctx on ROCm builds of torch)."""
 
-    def _noop(*args, **kwargs):
-        return None
+    __slots__ = ("_name",)
 
-    for name in _native.OP_NAMES:
-        try:
-            register(f"crumpet_ops::{name}")(_noop)
-        except (RuntimeError, AttributeError, ValueError):
-            pass
+    def __init__(self, name: str):
+        self._name = name
 
+    def __enter__(self):
+        torch.cuda.nvtx.range_push(self._name)
+        return self
 
-_register_fake_impls()
+    def __exit__(self, *exc) -> bool:
+        torch.cuda.nvtx.range_pop()
+        return False
 
 
-@contextlib.contextmanager
-def _range(name: str):
-    """roctx range around an op when CRUMPET_ENABLE_NVTX=1 (torch.cuda.nvtx is roctx on ROCm)."""
-    if os.environ.get("CRUMPET_ENABLE_NVTX", "0") == "1" and torch.cuda.is_available():
-        torch.cuda.nvtx.range_push(name)
-        try:
-            yield
-        finally:
-            torch.cuda.nvtx.range_pop()
-    else:
-        yield
+def _op_range(name: str):
+    """A roctx range around one op call when CRUMPET_ENABLE_NVTX=1 (none
+    while torch.compile traces)."""
+    if (os.environ.get("CRUMPET_ENABLE_NVTX", "0") != "1" or torch.compiler.is_compiling()
+            or not torch.cuda.is_available()):
+        return contextlib.nullcontext()
+    return _RoctxRange(name)
 
 
-def _triple(name: str, value: Sequence[int]) -> tuple[int, int, int]:
-    if len(value) != 3:
-        raise ValueError(f"{name} must contain exactly three values")
-    out = tuple(int(v) for v in value)
-    if any(v < 0 for v in out):
-        raise ValueError(f"{name} values must be non-negative")
-    return out
-
-
-def _validate_shape(D: int, H: int, W: int, window_size, shift_size) -> None:
-    if D <= 0 or H <= 0 or W <= 0:
-        raise ValueError("D, H and W must be positive")
-    if any(v <= 0 for v in window_size):
-        raise ValueError("window_size values must be positive")
-    if D % window_size[0] or H % window_size[1] or W % window_size[2]:
-        raise ValueError(
-            "standalone CRUMPET kernels require D, H and W to be divisible by window_size"
-        )
-    for axis, (shift, window) in enumerate(zip(shift_size, window_size)):
-        if shift < 0 or shift >= window:
-            raise ValueError(f"shift_size[{axis}] must satisfy 0 <= shift < window_size[{axis}]")
-
-
-def _check_dtype(dtype: torch.dtype) -> None:
-    if dtype not in _SUPPORTED_DTYPES:
-        raise TypeError("CRUMPET supports torch.float32, torch.float16 and torch.bfloat16")
-
-
-def _hip_ops(device: torch.device, what: str):
-    """The op namespace for a HIP tensor; raises for any other device."""
+def _device_ops(device: torch.device, what: str):
+    """The op namespace for a HIP tensor; any other device raises."""
     if device.type != "cuda":
         raise RuntimeError(
             f"{what}: crumpet_amd runs only on HIP (MI355X) devices; got a tensor on '{device}'"
         )
     return _native.ops()
-
-
-def _windows_geometry(D, H, W, window_size):
-    volume = window_size[0] * window_size[1] * window_size[2]
-    num_windows = (D // window_size[0]) * (H // window_size[1]) * (W // window_size[2])
-    return volume, num_windows
 
 
 def compute_attn_mask_3d(
@@ -127,76 +83,65 @@ def compute_attn_mask_3d(
     Cached per ``(D, H, W, window_size, shift_size, dtype, device)``
     (reference: torch-ext/crumpet/__init__.py:139-182).
     """
-    window_size = _triple("window_size", window_size)
-    shift_size = _triple("shift_size", shift_size)
-    _check_dtype(dtype)
-    D, H, W = int(D), int(H), int(W)
-    _validate_shape(D, H, W, window_size, shift_size)
+    window_size = as_triple("window_size", window_size)
+    shift_size = as_triple("shift_size", shift_size)
+    require_float_dtype(dtype)
+    grid = WindowGrid.checked(D, H, W, window_size, shift_size)
     dev = torch.device(device)
-    volume, num_windows = _windows_geometry(D, H, W, window_size)
+    shape = (grid.num_windows, grid.volume, grid.volume)
     if dev.type == "meta":
-        return torch.empty((num_windows, volume, volume), dtype=dtype, device=dev)
-    ops = _hip_ops(dev, "compute_attn_mask_3d")
+        return torch.empty(shape, dtype=dtype, device=dev)
+    ops = _device_ops(dev, "compute_attn_mask_3d")
 
-    def compute() -> torch.Tensor:
-        out = torch.empty((num_windows, volume, volume), dtype=dtype, device=dev)
-        with _range("crumpet.compute_attn_mask_3d"):
-            ops.compute_attn_mask_3d(out, D, H, W, *window_size, *shift_size)
-        return out
+    def build() -> torch.Tensor:
+        mask = torch.empty(shape, dtype=dtype, device=dev)
+        with _op_range("crumpet.compute_attn_mask_3d"):
+            ops.compute_attn_mask_3d(mask, *grid.dims, *grid.op_args)
+        return mask
 
-    return get_or_compute_mask(make_mask_key(D, H, W, window_size, shift_size, dtype, dev), compute)
-
-
-class _ShiftPartitionFn(torch.autograd.Function):
-    """Partition forward; backward is the inverse gather (adjoint of a permutation)."""
-
-    @staticmethod
-    def forward(ctx, x, window_size, shift_size):
-        x = x.contiguous()
-        B, D, H, W, C = (int(v) for v in x.shape)
-        volume, num_windows = _windows_geometry(D, H, W, window_size)
-        out = torch.empty((B * num_windows, volume, C), dtype=x.dtype, device=x.device)
-        _native.ops().fused_shift_partition_3d(out, x, *window_size, *shift_size)
-        ctx.shape = (B, D, H, W, C)
-        ctx.window_size = window_size
-        ctx.shift_size = shift_size
-        return out
-
-    @staticmethod
-    def backward(ctx, grad_output):
-        B, D, H, W, C = ctx.shape
-        grad_x = torch.empty((B, D, H, W, C), dtype=grad_output.dtype, device=grad_output.device)
-        _native.ops().fused_shift_partition_3d_backward(
-            grad_x, grad_output.contiguous(), B, D, H, W, C, *ctx.window_size, *ctx.shift_size
-        )
-        return grad_x, None, None
+    key = make_mask_key(*grid.dims, grid.window, grid.shift, dtype, dev)
+    return get_or_compute_mask(key, build)
 
 
-class _UnshiftUnpartitionFn(torch.autograd.Function):
-    """Unpartition forward; backward is the partition gather."""
+def _to_windows(x: torch.Tensor, grid: WindowGrid) -> torch.Tensor:
+    """Shift-partition gather of a contiguous ``[B, D, H, W, C]`` volume."""
+    batch, channels = x.shape[0], x.shape[4]
+    out = x.new_empty(grid.windows_shape(batch, channels))
+    _native.ops().fused_shift_partition_3d(out, x, *grid.op_args)
+    return out
+
+
+def _to_volume(windows: torch.Tensor, grid: WindowGrid, batch: int) -> torch.Tensor:
+    """Unshift-unpartition gather of contiguous ``[B*nW, vol, C]`` windows."""
+    channels = windows.shape[2]
+    out = windows.new_empty(grid.volume_shape(batch, channels))
+    _native.ops().fused_unshift_unpartition_3d(out, windows, batch, *grid.dims, channels, *grid.op_args)
+    return out
+
+
+class _WindowPermute(torch.autograd.Function):
+    """One of the two window permutations with autograd.
+
+    Partition and unpartition are permutations of the same elements, each
+    the inverse of the other, so the gradient of one is the other applied to
+    the incoming gradient (the reference's ``*_backward`` ops are exactly
+    these gathers, torch_binding.cpp:22-24,29-31).
+    """
 
     @staticmethod
-    def forward(ctx, windows, B, D, H, W, C, window_size, shift_size):
-        windows = windows.contiguous()
-        out = torch.empty((B, D, H, W, C), dtype=windows.dtype, device=windows.device)
-        _native.ops().fused_unshift_unpartition_3d(
-            out, windows, B, D, H, W, C, *window_size, *shift_size
-        )
-        ctx.window_size = window_size
-        ctx.shift_size = shift_size
-        return out
+    def forward(ctx, src: torch.Tensor, grid: WindowGrid, to_windows: bool, batch: int):
+        ctx.grid, ctx.to_windows, ctx.batch = grid, to_windows, batch
+        src = src.contiguous()
+        return _to_windows(src, grid) if to_windows else _to_volume(src, grid, batch)
 
     @staticmethod
-    def backward(ctx, grad_output):
-        B, D, H, W, C = (int(v) for v in grad_output.shape)
-        volume, num_windows = _windows_geometry(D, H, W, ctx.window_size)
-        grad_windows = torch.empty(
-            (B * num_windows, volume, C), dtype=grad_output.dtype, device=grad_output.device
-        )
-        _native.ops().fused_unshift_unpartition_3d_backward(
-            grad_windows, grad_output.contiguous(), *ctx.window_size, *ctx.shift_size
-        )
-        return grad_windows, None, None, None, None, None, None, None
+    def backward(ctx, grad: torch.Tensor):
+        grad = grad.contiguous()
+        if ctx.to_windows:
+            grad_src = _to_volume(grad, ctx.grid, ctx.batch)
+        else:
+            grad_src = _to_windows(grad, ctx.grid)
+        return grad_src, None, None, None
 
 
 def fused_shift_partition_3d(
@@ -211,21 +156,18 @@ def fused_shift_partition_3d(
     """
     if x.ndim != 5:
         raise ValueError("x must have shape [B, D, H, W, C]")
-    window_size = _triple("window_size", window_size)
-    shift_size = _triple("shift_size", shift_size)
-    _check_dtype(x.dtype)
-    B, D, H, W, C = (int(v) for v in x.shape)
-    _validate_shape(D, H, W, window_size, shift_size)
-    volume, num_windows = _windows_geometry(D, H, W, window_size)
+    window_size = as_triple("window_size", window_size)
+    shift_size = as_triple("shift_size", shift_size)
+    require_float_dtype(x.dtype)
+    batch, D, H, W, channels = (int(v) for v in x.shape)
+    grid = WindowGrid.checked(D, H, W, window_size, shift_size)
     if x.device.type == "meta":
-        return torch.empty((B * num_windows, volume, C), dtype=x.dtype, device=x.device)
-    ops = _hip_ops(x.device, "fused_shift_partition_3d")
-    with _range("crumpet.fused_shift_partition_3d"):
+        return x.new_empty(grid.windows_shape(batch, channels))
+    _device_ops(x.device, "fused_shift_partition_3d")
+    with _op_range("crumpet.fused_shift_partition_3d"):
         if torch.is_grad_enabled() and x.requires_grad:
-            return _ShiftPartitionFn.apply(x, window_size, shift_size)
-        out = torch.empty((B * num_windows, volume, C), dtype=x.dtype, device=x.device)
-        ops.fused_shift_partition_3d(out, x.contiguous(), *window_size, *shift_size)
-        return out
+            return _WindowPermute.apply(x, grid, True, batch)
+        return _to_windows(x.contiguous(), grid)
 
 
 def fused_unshift_unpartition_3d(
@@ -244,28 +186,21 @@ def fused_unshift_unpartition_3d(
     """
     if windows.ndim != 3:
         raise ValueError("windows must have shape [B * num_windows, window_volume, C]")
-    window_size = _triple("window_size", window_size)
-    shift_size = _triple("shift_size", shift_size)
-    _check_dtype(windows.dtype)
-    B, D, H, W, C = (int(B), int(D), int(H), int(W), int(C))
-    _validate_shape(D, H, W, window_size, shift_size)
-    volume, num_windows = _windows_geometry(D, H, W, window_size)
-    expected = (B * num_windows, volume, C)
+    window_size = as_triple("window_size", window_size)
+    shift_size = as_triple("shift_size", shift_size)
+    require_float_dtype(windows.dtype)
+    grid = WindowGrid.checked(D, H, W, window_size, shift_size)
+    batch, channels = int(B), int(C)
+    expected = grid.windows_shape(batch, channels)
     if tuple(int(v) for v in windows.shape) != expected:
         raise ValueError(f"windows must have shape {expected}")
     if windows.device.type == "meta":
-        return torch.empty((B, D, H, W, C), dtype=windows.dtype, device=windows.device)
-    ops = _hip_ops(windows.device, "fused_unshift_unpartition_3d")
-    with _range("crumpet.fused_unshift_unpartition_3d"):
+        return windows.new_empty(grid.volume_shape(batch, channels))
+    _device_ops(windows.device, "fused_unshift_unpartition_3d")
+    with _op_range("crumpet.fused_unshift_unpartition_3d"):
         if torch.is_grad_enabled() and windows.requires_grad:
-            return _UnshiftUnpartitionFn.apply(
-                windows, B, D, H, W, C, window_size, shift_size
-            )
-        out = torch.empty((B, D, H, W, C), dtype=windows.dtype, device=windows.device)
-        ops.fused_unshift_unpartition_3d(
-            out, windows.contiguous(), B, D, H, W, C, *window_size, *shift_size
-        )
-        return out
+            return _WindowPermute.apply(windows, grid, False, batch)
+        return _to_volume(windows.contiguous(), grid, batch)
 
 
 def patch_monai_swin_unetr() -> bool:

@@ -68,6 +68,24 @@ def _load() -> None:
         _ops = torch.ops.crumpet_ops
     except (OSError, RuntimeError) as exc:  # pragma: no cover - depends on the build
         _error = f"{type(exc).__name__}: {exc}"
+        return
+    _declare_fake_kernels()
+
+
+def _mutating_op_fake(*args, **kwargs) -> None:
+    """Every crumpet_ops op writes into a caller-allocated output and returns
+    nothing, so its fake (meta) kernel has nothing to do."""
+    return None
+
+
+def _declare_fake_kernels() -> None:
+    """Fake kernels for FakeTensor / torch.compile tracing of the ops (the
+    reference registers the same no-op fakes: torch-ext/crumpet/__init__.py:50-73)."""
+    for name in OP_NAMES:
+        try:
+            torch.library.register_fake(f"crumpet_ops::{name}")(_mutating_op_fake)
+        except (RuntimeError, ValueError):
+            pass  # already registered in this process
 
 
 def ops():

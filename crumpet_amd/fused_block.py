@@ -29,30 +29,17 @@ from typing import Sequence
 import torch
 
 from . import _native
+from ._geometry import as_triple, padded_dims, require_float_dtype
 from .fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
-
-_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
-
-
-def _triple(name: str, value: Sequence[int]) -> tuple[int, int, int]:
-    if len(value) != 3:
-        raise ValueError(f"{name} must contain exactly three values")
-    return tuple(int(v) for v in value)
-
-
-def _padded(dims, window_size):
-    return tuple(-(-d // w) * w for d, w in zip(dims, window_size))
-
-
-def _num_windows(padded, window_size):
-    return (padded[0] // window_size[0]) * (padded[1] // window_size[1]) * (padded[2] // window_size[2])
-
 
 def _check(x: torch.Tensor, what: str) -> None:
     if x.device.type != "cuda":
         raise RuntimeError(f"{what}: crumpet_amd runs only on HIP (MI355X) devices; got '{x.device}'")
-    if x.dtype not in _DTYPES:
-        raise TypeError("CRUMPET supports torch.float32, torch.float16 and torch.bfloat16")
+    require_float_dtype(x.dtype)
+
+
+def _num_windows(padded, window_size):
+    return (padded[0] // window_size[0]) * (padded[1] // window_size[1]) * (padded[2] // window_size[2])
 
 
 def window_qkv_3d(
@@ -73,15 +60,14 @@ def window_qkv_3d(
     ``weight``/``bias``, in ``dtype`` (default ``x.dtype``; ``weight`` and
     ``bias`` are cast to it, as autocast casts a Linear's parameters)."""
     _check(x, "window_qkv_3d")
-    ws = _triple("window_size", window_size)
-    ss = _triple("shift_size", shift_size)
+    ws = as_triple("window_size", window_size, signed=True)
+    ss = as_triple("shift_size", shift_size, signed=True)
     if x.dim() != 5:
         raise ValueError("x must have shape [B, D, H, W, C]")
     dtype = x.dtype if dtype is None else dtype
-    if dtype not in _DTYPES:
-        raise TypeError("CRUMPET supports torch.float32, torch.float16 and torch.bfloat16")
+    require_float_dtype(dtype)
     B, D, H, W, _ = x.shape
-    padded = _padded((D, H, W), ws)
+    padded = padded_dims((D, H, W), ws)
     n = ws[0] * ws[1] * ws[2]
     w = weight.to(dtype).contiguous()
     b = bias.to(dtype).contiguous() if bias is not None else None
@@ -108,8 +94,8 @@ def window_proj_3d(
     order (inverse partition over the padded grid, shift by ``+shift_size``)
     and cropped to ``D, H, W``; in the dtype of ``windows``."""
     _check(windows, "window_proj_3d")
-    ws = _triple("window_size", window_size)
-    ss = _triple("shift_size", shift_size)
+    ws = as_triple("window_size", window_size, signed=True)
+    ss = as_triple("shift_size", shift_size, signed=True)
     dtype = windows.dtype
     w = weight.to(dtype).contiguous()
     b = bias.to(dtype).contiguous() if bias is not None else None
@@ -139,12 +125,12 @@ def fused_window_msa_3d(
     volume's geometry (``region=True``, nothing is read) or taken from
     ``mask`` (``[nW, N, N]``, window b reads ``mask[b mod nW]``).
     """
-    ws = _triple("window_size", window_size)
-    ss = _triple("shift_size", shift_size)
+    ws = as_triple("window_size", window_size, signed=True)
+    ss = as_triple("shift_size", shift_size, signed=True)
     B, D, H, W, C = x.shape
     dtype = x.dtype if dtype is None else dtype
     hd = C // num_heads
-    padded = _padded((D, H, W), ws)
+    padded = padded_dims((D, H, W), ws)
     n = ws[0] * ws[1] * ws[2]
     qkv_out = window_qkv_3d(x, qkv.weight, qkv.bias, ws, ss, norm.weight, norm.bias, norm.eps, True, dtype)
     nwin = qkv_out.shape[0]

@@ -3,7 +3,7 @@
 Mirrors tests/test_compile.py:9-22 of the reference (a fullgraph-compiled
 partition -> unpartition round trip must return its input) and checks each
 crumpet_ops schema with opcheck: schema and mutation annotations, the fake
-(meta) kernels registered in crumpet_amd/__init__.py, and AOT dispatch.
+(meta) kernels registered in crumpet_amd/_native.py, and AOT dispatch.
 The compile test uses the aot_eager backend: it traces through Dynamo, fake
 tensors and AOTAutograd exactly as inductor would, without generating any
 kernels of its own, so the ops run as the HIP kernels they are.
