@@ -505,8 +505,9 @@ def bench_e2e(args, dev):
                         "median of iters forwards"}
 
 
-def cpu_baseline():
-    """Oracle (C scalar, 1 thread) round trip on the full config-1 volume."""
+def cpu_scalar_oracle():
+    """The C oracle's scalar round trip (1 thread) on the full config-1 volume,
+    reported beside the reference's eager CPU path."""
     import numpy as np
 
     from oracle import oracle
@@ -551,13 +552,32 @@ def _cpu_attention(q, k, v, bias, mask, scale):
     return torch.softmax(s, dim=-1) @ v
 
 
+def cpu_mask_where(D, H, W, ws, ss, dtype):
+    """The vectorised eager mask of torch-ext/crumpet/reference.py:50-98, in
+    torch on the CPU: per-axis region labels (0 below D - ws, 1 below D - ss,
+    else 2) combined as 9 r_d + 3 r_h + r_w, window partition, pairwise
+    comparison of the labels, -100 where they differ."""
+    import torch
+
+    from crumpet_amd import swin_unetr_compat as sw
+
+    def regions(n, w, s):
+        a = torch.arange(n)
+        return torch.where(a < n - w, 0, torch.where(a < n - s, 1, 2))
+
+    labels = (9 * regions(D, ws[0], ss[0])[:, None, None] + 3 * regions(H, ws[1], ss[1])[None, :, None]
+              + regions(W, ws[2], ss[2])[None, None, :]).to(torch.int16)
+    win = sw.window_partition(labels.view(1, D, H, W, 1), ws)[..., 0]
+    differ = win[:, None, :] != win[:, :, None]
+    return torch.where(differ, torch.tensor(-100.0, dtype=dtype), torch.tensor(0.0, dtype=dtype))
+
+
 def cpu_eager_paths(skip_e2e=False):
     """The reference's eager paths timed on the host cores, one per config,
     each on a bounded sample stated in its entry (reported baselines only,
     never targets): torch roll + view/permute (config 1), the two eager mask
     constructions (config 2), the fp32 attention chain (configs 3 and 4) and
     the unpatched fp32 Swin UNETR forward (config 5)."""
-    import numpy as np
     import torch
 
     from crumpet_amd import swin_unetr_compat as sw
@@ -579,15 +599,20 @@ def cpu_eager_paths(skip_e2e=False):
                                   "median of 3"}
     del x
 
-    # config 2: MONAI-style slice construction and the vectorised where, at
-    # D=49 (343 windows, 1/8 of config 2's elements); GB/s of fp16 output
-    n49 = 343 * 343 * 343 * 2
-    t_monai = _cpu_median(lambda: oracle.np_mask_monai_slices(49, 49, 49, (7, 7, 7), (3, 3, 3)).astype(np.float16), 3)
-    t_where = _cpu_median(lambda: np.where(oracle.np_mask_where(49, 49, 49, (7, 7, 7), (3, 3, 3)),
-                                           np.float16(-100), np.float16(0)), 3)
-    res["mask"] = {"ms_monai_slices": round(t_monai * 1e3, 2), "ms_where": round(t_where * 1e3, 2),
-                   "GB_s": round(n49 / min(t_monai, t_where) / 1e9, 3), "threads": 1,
-                   "sample": "D=49 (343 windows x 343^2, 80.7 MB fp16 out), numpy, median of 3"}
+    # config 2 at full size: the MONAI slice-assignment construction
+    # (benchmarks/bench_kernel.py:63-86, as MONAI's compute_mask in the compat
+    # model, fp32 then cast) and the vectorised where (reference.py:50-98),
+    # fp16 [2744, 343, 343]; GB/s of fp16 output.  The two agree bit for bit.
+    ws7, ss3 = (7, 7, 7), (3, 3, 3)
+    t_monai = _cpu_median(lambda: sw.compute_mask((98, 98, 98), ws7, ss3, "cpu").to(torch.float16), 2)
+    t_where = _cpu_median(lambda: cpu_mask_where(98, 98, 98, ws7, ss3, torch.float16), 2)
+    same = torch.equal(sw.compute_mask((98, 98, 98), ws7, ss3, "cpu").to(torch.float16),
+                       cpu_mask_where(98, 98, 98, ws7, ss3, torch.float16))
+    res["mask"] = {"ms_monai_slices": round(t_monai * 1e3, 1), "ms_where": round(t_where * 1e3, 1),
+                   "GB_s": round(C2_BYTES / min(t_monai, t_where) / 1e9, 3), "threads": threads,
+                   "constructions_equal": same,
+                   "sample": "full config 2 (98^3, [2744,343,343] fp16, 645.7 MB out), torch on the CPU, "
+                             "median of 2 each"}
 
     # config 3: fp32 eager attention on every 14th window (98 of 1372)
     g = torch.Generator().manual_seed(300)
@@ -848,8 +873,15 @@ def main():
         "components": components,
     }
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline()
         cpu = cpu_eager_paths(skip_e2e=args.no_e2e)
+        rt = cpu["roundtrip"]
+        line["cpu_baseline"] = {
+            "value": rt["GB_s"], "unit": "GB/s", "cores": rt["threads"], "kind": "port",
+            "sample": "the reference's eager CPU path for config 1 (torch-ext/crumpet/reference.py:141-184): "
+                      "torch.roll + view/permute window partition and window reverse + roll back, fp16, "
+                      f"full [1,98^3,48] volume, median of 3 round trips ({rt['ms']} ms), "
+                      f"{rt['threads']} torch threads"}
+        line["cpu_baseline_scalar_oracle"] = cpu_scalar_oracle()
         components["partition"]["cpu_eager_roundtrip"] = cpu["roundtrip"]
         components["mask"]["cpu_eager"] = cpu["mask"]
         if "attention" in components:
