@@ -73,6 +73,9 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     if (bias_strides[2] != 1 || bias_strides[0] < 0 || bias_strides[1] < 0)
         return fail(CRUMPET_ERR_INVALID_ARGUMENT,
                     "%s: bias must have unit stride along keys", what);
+    // rows are read with multi-element loads: they must not overlap
+    if (N > 1 && bias_strides[1] < N)
+        return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: bias rows must not overlap (row stride < N)", what);
     if (((N - 1) * bias_strides[1] + N) * dtype_size(bias_dtype) >= (int64_t(1) << 31))
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: bias row stride out of range", what);
     if (mask != nullptr) {
@@ -87,6 +90,9 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         if (mask_strides[0] < 0 || mask_strides[1] < 0 ||
             ((N - 1) * mask_strides[1] + N) * 4 >= (int64_t(1) << 31))
             return fail(CRUMPET_ERR_UNSUPPORTED, "%s: mask row stride out of range", what);
+        if (N > 1 && mask_strides[1] < N)
+            return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: mask rows must not overlap (row stride < N)",
+                        what);
         if (mask_batch <= 0 || B % mask_batch != 0)
             return fail(CRUMPET_ERR_INVALID_ARGUMENT,
                         "%s: mask batch %lld must divide the window batch %lld", what,

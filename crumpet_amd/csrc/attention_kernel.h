@@ -606,15 +606,134 @@ struct Stage<T, NT, true> {
 
 // Bias (+ region mask) tiles of one strip, built in registers from the
 // caller's bias tensor: lane (col, g) holds keys 16t + 4g + r of query qi.
-// The head's [N, N] bias is read through a buffer descriptor, so every load
-// is one instruction with an immediate offset; keys past N read 0 or the
-// next row and are replaced by -inf (probability exactly 0).  Padded query
-// rows get 0 (never stored).  In region mode a key whose shift-region class
-// differs from the query's on an axis that the window type `code` splits
-// gets -100.  Runs when the window type changes (at most 8 times per
-// workgroup), never per window.  kLog2: the tiles are kept in log2 units
+// The head's [N, N] bias is read through a buffer descriptor; keys past N
+// read 0 or the next row and are replaced by -inf (probability exactly 0).
+// Padded query rows get 0 (never stored).  In region mode a key whose
+// shift-region class differs from the query's on an axis that the window
+// type `code` splits gets -100.  kLog2: the tiles are kept in log2 units
 // (multiplied by log2(e)) plus the query's row offset `off`, for the offset
-// softmax of the 2-byte types (attend_offset).
+// softmax of the 2-byte types (attend_offset).  Runs when the window type
+// changes (at most 8 times per workgroup) or the offsets move, never per
+// window otherwise.
+//
+// A lane's 4 keys of a tile are consecutive in its bias row, so each tile
+// is one load, and all of a wave's loads are issued before any is used (one
+// memory round trip per build).  16-bit rows of an odd row stride start in
+// the middle of a dword and unaligned loads are slow, so those lanes load
+// the three dwords around their keys from a dword-aligned offset and shift
+// the halves into place (shift: 0 or 16 bits).  The last tile of row N-1
+// can reach past the descriptor's extent, where a range check at dword
+// granularity could zero in-range keys: those lanes read that tile again
+// element by element.  (Bias rows never overlap: the host checks that the
+// row stride is at least N.)
+template <int NT, int kMask, bool kLog2, int kBiasDtype>
+__device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_rsrc_t rs, int N, int64_t bsd1,
+                                               int qi, int g, int code, const uint8_t* cls, float off) {
+    constexpr int kEs = kBiasDtype == CRUMPET_DTYPE_F32 ? 4 : 2;
+    // Opaque copies of the lane's position and N: what the build derives from
+    // them (per-key validity, offsets) is then computed here, each time,
+    // instead of being hoisted out of the window loop and held in registers
+    // that the attention loop needs.
+    asm volatile("" : "+v"(qi), "+v"(g), "+s"(N));
+    const bool row = qi < N;
+    const int qr = row ? qi : N - 1;
+    const int e0 = static_cast<int>(int64_t(qr) * bsd1 + 4 * g);  // element offset of tile 0's keys
+    constexpr int kTileBytes = 16 * kEs;
+    constexpr int kWords = kEs == 4 ? 4 : 3;
+    const int shift = kEs == 2 ? (e0 & 1) * 16 : 0;
+    const int voff = kEs == 2 ? (e0 & ~1) * 2 : e0 * 4;
+    uint32_t cq = 0, cmask = 0;
+    if constexpr (kMask == kMaskRegion) {
+        cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
+        cmask = uint32_t(code) * 0x01010101u;
+    }
+    // Two halves of the tiles, each: all loads, then the conversions (the
+    // raw words of every tile at once would not fit next to the tiles).
+    constexpr int kHalf = (NT + 1) / 2;
+#pragma unroll
+    for (int t0 = 0; t0 < NT; t0 += kHalf) {
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t raw[kHalf][kWords];
+#pragma unroll
+        for (int u = 0; u < kHalf; ++u) {
+            const int t = t0 + u;
+            if (t >= NT) break;
+            if constexpr (kEs == 4) {
+                const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + kTileBytes * t, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) raw[u][i] = w[i];
+            } else {
+                const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rs, voff + kTileBytes * t, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 3; ++i) raw[u][i] = w[i];
+            }
+        }
+        constexpr int tl = NT - 1;
+        if (tl >= t0 && tl < t0 + kHalf && qr == N - 1 && 16 * tl + 4 * g + 3 >= N) {
+            // the end-of-extent tile, element by element, laid out as the
+            // vector load would have returned it
+            const int u = tl - t0;
+            if constexpr (kEs == 4) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    raw[u][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + kTileBytes * tl + 4 * r, 0, 0);
+            } else {
+                uint32_t kv[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    kv[r] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + shift / 8 + kTileBytes * tl + 2 * r, 0, 0);
+                if (shift != 0) {
+                    raw[u][0] = kv[0] << 16;
+                    raw[u][1] = kv[1] | (kv[2] << 16);
+                    raw[u][2] = kv[3];
+                } else {
+                    raw[u][0] = kv[0] | (kv[1] << 16);
+                    raw[u][1] = kv[2] | (kv[3] << 16);
+                    raw[u][2] = 0u;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kHalf; ++u) {
+            const int t = t0 + u;
+            if (t >= NT) break;
+            // one tile at a time: scheduled together, the per-key lane masks
+            // of all tiles would not fit the scalar registers
+            __builtin_amdgcn_sched_barrier(0);
+            uint32_t split = 0;  // byte r nonzero: key 16t+4g+r is masked by the region rule
+            if constexpr (kMask == kMaskRegion)
+                split = (*reinterpret_cast<const uint32_t*>(&cls[16 * t + 4 * g]) ^ cq) & cmask;
+            float v4[4];
+            if constexpr (kEs == 4) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v4[r] = __uint_as_float(raw[u][r]);
+            } else {
+                const uint32_t hw[2] = {__builtin_amdgcn_alignbit(raw[u][1], raw[u][0], shift),
+                                        __builtin_amdgcn_alignbit(raw[u][2], raw[u][1], shift)};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t bits = (r & 1) ? hw[r >> 1] >> 16 : hw[r >> 1] & 0xffffu;
+                    if constexpr (kBiasDtype == CRUMPET_DTYPE_BF16)
+                        v4[r] = __uint_as_float(bits << 16);
+                    else
+                        v4[r] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float val = v4[r];
+                if constexpr (kMask == kMaskRegion) {
+                    if ((split >> (8 * r)) & 0xffu) val += -100.0f;
+                }
+                if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
+                val = row ? val : 0.0f;
+                bs[t][r] = (16 * t + 4 * g + r) < N ? val : -INFINITY;
+            }
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 template <int NT, int kMask, bool kLog2>
 __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, int h, int qi, int g,
                                             int code, const uint8_t* cls, float off) {
@@ -630,51 +749,20 @@ __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, 
     const int bias_dtype = pp->bias_dtype;
     const int64_t bsd0 = pp->bsd[0], bsd1 = pp->bsd[1];
     const void* bias_ptr = pp->bias;
-    const bool row = qi < N;
-    const int qr = row ? qi : N - 1;
     const int es = bias_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
-    const bool bf16 = bias_dtype == CRUMPET_DTYPE_BF16;
     // base and extent are workgroup-uniform; readfirstlane keeps the
     // descriptor in SGPRs (a VGPR descriptor costs a waterfall loop per load)
     char* hb = uniform_ptr(static_cast<const char*>(bias_ptr) + int64_t(h) * bsd0 * es);
     const int extent =
         __builtin_amdgcn_readfirstlane(static_cast<int>((int64_t(N - 1) * bsd1 + N) * es));
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(hb, 0, extent, 0x00020000);
-    const int voff = static_cast<int>((int64_t(qr) * bsd1 + 4 * g) * es);
-    uint32_t cq = 0, cmask = 0;
-    if constexpr (kMask == kMaskRegion) {
-        cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
-        cmask = uint32_t(code) * 0x01010101u;
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-        uint32_t split = 0;  // byte r nonzero: key 16t+4g+r is masked by the region rule
-        if constexpr (kMask == kMaskRegion)
-            split = (*reinterpret_cast<const uint32_t*>(&cls[16 * t + 4 * g]) ^ cq) & cmask;
-        float v4[4];
-        if (es == 4) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                v4[r] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, voff + (16 * t + r) * 4, 0, 0));
-        } else {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t bits = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + (16 * t + r) * 2, 0, 0);
-                const float fh = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-                v4[r] = bf16 ? __uint_as_float(bits << 16) : fh;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            float val = v4[r];
-            if constexpr (kMask == kMaskRegion) {
-                if ((split >> (8 * r)) & 0xffu) val += -100.0f;
-            }
-            if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
-            val = row ? val : 0.0f;
-            bs[t][r] = (16 * t + 4 * g + r) < N ? val : -INFINITY;
-        }
-    }
+    // uniform: one dtype branch per build, none per tile or element
+    if (bias_dtype == CRUMPET_DTYPE_F32)
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F32>(bs, rs, N, bsd1, qi, g, code, cls, off);
+    else if (bias_dtype == CRUMPET_DTYPE_BF16)
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_BF16>(bs, rs, N, bsd1, qi, g, code, cls, off);
+    else
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F16>(bs, rs, N, bsd1, qi, g, code, cls, off);
 }
 
 

@@ -152,7 +152,8 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
     int64_t ms[3] = {0, 0, 0};
     at::Tensor mask_t;
     if (mask.has_value()) {
-        mask_t = mask->stride(2) == 1 ? *mask : mask->contiguous();
+        // the kernels read mask rows with unit key stride, rows not overlapping
+        mask_t = (mask->stride(2) == 1 && (N < 2 || mask->stride(1) >= N)) ? *mask : mask->contiguous();
         const at::Tensor& m = mask_t;
         TORCH_CHECK(m.device() == dev, what, ": mask must be on the same device");
         TORCH_CHECK(m.dim() == 3 && m.size(1) == N && m.size(2) == N, what,
@@ -185,8 +186,8 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
         vs[i] = v.stride(i);
         os[i] = out.stride(i);
     }
-    // the kernel reads bias rows through unit key stride
-    const at::Tensor bk = bias.stride(2) == 1 ? bias : bias.contiguous();
+    // the kernels read bias rows with unit key stride, rows not overlapping
+    const at::Tensor bk = (bias.stride(2) == 1 && (N < 2 || bias.stride(1) >= N)) ? bias : bias.contiguous();
     for (int i = 0; i < 3; ++i) bs[i] = bk.stride(i);
     check_status(crumpet_fused_swin_attention(
         out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
@@ -225,7 +226,8 @@ void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at
         vs[i] = v.stride(i);
         os[i] = out.stride(i);
     }
-    const at::Tensor bk = bias.stride(2) == 1 ? bias : bias.contiguous();
+    // the kernels read bias rows with unit key stride, rows not overlapping
+    const at::Tensor bk = (bias.stride(2) == 1 && (N < 2 || bias.stride(1) >= N)) ? bias : bias.contiguous();
     for (int i = 0; i < 3; ++i) bs[i] = bk.stride(i);
     check_status(crumpet_fused_swin_attention_shifted(
         out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,

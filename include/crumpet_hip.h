@@ -161,16 +161,19 @@ CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  *
  * q, k, v, out : [B, Hh, N, Dh] with arbitrary element strides (in elements,
  *                order b, h, n, d); dtype F16, BF16 or F32 (all four equal).
- * bias         : [Hh, N, N], strides (h, i, j) with unit j stride, dtype
+ * bias         : [Hh, N, N], strides (h, i, j) with unit j stride and a
+ *                row stride i of at least N (rows do not overlap), dtype
  *                F32/F16/BF16.
  * mask         : [mask_batch, N, N] or NULL; strides (m, i, j) with unit j
- *                stride; mask_batch
+ *                stride and a row stride of at least N; mask_batch
  *                must divide B (1 broadcasts, B is per window, nW repeats
  *                the per-window masks over an outer batch).
  * boundary     : [B] uint8 or NULL.  When NULL and mask != NULL every window
  *                reads its mask; a zero flag skips the mask for that window.
- * scale        : softmax scale; q is multiplied by it in fp32 and rounded
- *                back to the input type before the product.
+ * scale        : softmax scale.  fp32 operands: q is multiplied by it and
+ *                rounded back.  2-byte operands: q * scale * log2(e) enters
+ *                the product as a rounded value plus its rounded remainder,
+ *                which is at least as precise as the rounded q * scale.
  *
  * Needs no workspace: every buffer is an input or the output.
  *

@@ -123,6 +123,35 @@ def test_mask_repeat_by_window_index(oracle, dev):
 
 
 @pytest.mark.parametrize("N", [27, 125, 343])
+@pytest.mark.parametrize("bdt", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+def test_bias_row_strides(oracle, dev, bdt, N):
+    """The bias read through padded rows (odd row stride N + 3, so 16-bit rows
+    start mid-dword) and through broadcast rows (row stride 0; the op makes
+    such a bias contiguous, as it does a broadcast-row mask): every key's
+    value reaches the scores, the last keys of the last row included.  Bias
+    values ~N(0, 2) make a wrong or missing value visible."""
+    dtype = torch.bfloat16 if bdt == torch.bfloat16 else torch.float16
+    B, H, Dh = 4, 2, 16
+    q, k, v = _inputs(B, H, N, Dh, dtype, 950 + N)
+    g = torch.Generator().manual_seed(951 + N)
+    wide = (torch.randn((H, N, N + 3), generator=g) * 2.0).to(bdt)
+    row = (torch.randn((H, 1, N), generator=g) * 2.0).to(bdt)
+    mrow = (torch.randn((1, 1, N), generator=g) * 3.0).to(dtype)
+    cases = (
+        ("padded bias rows", wide[:, :, :N], wide.to(dev)[:, :, :N], None, None),
+        ("broadcast rows", row.expand(H, N, N), row.to(dev).expand(H, N, N),
+         mrow.expand(1, N, N), mrow.to(dev).expand(1, N, N)),
+    )
+    for what, b_cpu, b_dev, m_cpu, m_dev in cases:
+        if "padded" in what:
+            assert b_dev.stride() == (N * (N + 3), N + 3, 1)
+        ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(b_cpu), None if m_cpu is None else _f32(m_cpu),
+                               None, scale=0.25)
+        out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), b_dev, m_dev, None, scale=0.25)
+        _compare(out, ref, dtype, f"{what} {bdt} N={N}")
+
+
+@pytest.mark.parametrize("N", [27, 125, 343])
 @pytest.mark.parametrize("mdt", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
 def test_random_mask_dtypes_and_odd_row_stride(oracle, dev, mdt, N):
     """Arbitrary mask values in every position, the mask a column slice of a

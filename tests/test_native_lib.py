@@ -82,19 +82,30 @@ def test_attention_argument_checks_need_no_gpu():
     fake = ctypes.c_void_p(256)
 
     def call(dtype=1, B=2, H=3, N=343, Dh=16, mask=None, mb=1):
+        rows = (ctypes.c_int64 * 3)(N * N, N, 1)
         return lib.crumpet_fused_swin_attention(
-            fake, s4, fake, s4, fake, s4, fake, s4, dtype, B, H, N, Dh, fake, 1, s3,
-            mask, 1, mb, s3, None, ctypes.c_float(0.25), None)
+            fake, s4, fake, s4, fake, s4, fake, s4, dtype, B, H, N, Dh, fake, 1, rows,
+            mask, 1, mb, rows, None, ctypes.c_float(0.25), None)
 
     assert call(Dh=8) == 2
     assert call(Dh=24) == 2 and b"head_dim 24" in lib.crumpet_last_error()
     assert call(dtype=5) == 1
     assert call(mask=fake, mb=3) == 1  # mask batch must divide B
     assert call(B=0) == 0
+    # bias and mask rows are read with multi-element loads: overlapping rows
+    # (row stride below N) are rejected; the torch op makes them contiguous
+    s3_rows = (ctypes.c_int64 * 3)(343 * 343, 343, 1)
+    st = lib.crumpet_fused_swin_attention(fake, s4, fake, s4, fake, s4, fake, s4, 1, 2, 3, 343, 16, fake, 1,
+                                          s3, None, 1, 1, s3, None, ctypes.c_float(0.25), None)
+    assert st == 1 and b"bias rows must not overlap" in lib.crumpet_last_error()
+    st = lib.crumpet_fused_swin_attention(fake, s4, fake, s4, fake, s4, fake, s4, 1, 2, 3, 343, 16, fake, 1,
+                                          s3_rows, fake, 1, 1, s3, None, ctypes.c_float(0.25), None)
+    assert st == 1 and b"mask rows must not overlap" in lib.crumpet_last_error()
 
     def shifted(B=8, N=343, D=14, ws=7, ss=3):
+        bias_s = (ctypes.c_int64 * 3)(N * N, N, 1)
         return lib.crumpet_fused_swin_attention_shifted(
-            fake, s4, fake, s4, fake, s4, fake, s4, 1, B, 3, N, 16, fake, 1, s3,
+            fake, s4, fake, s4, fake, s4, fake, s4, 1, B, 3, N, 16, fake, 1, bias_s,
             D, D, D, ws, ws, ws, ss, ss, ss, ctypes.c_float(0.25), None)
 
     assert shifted(D=15) == 1 and b"divisible" in lib.crumpet_last_error()
