@@ -21,6 +21,8 @@ namespace {
 // vector-IO kernels run 3 waves per SIMD); a partial last round costs more
 // than the extra prologues of smaller ranges.
 constexpr int64_t kTargetWorkgroups = 1536;
+// kHeadsPerWg workgroups take one CU's LDS each: one per CU
+constexpr int64_t kTargetWorkgroupsMultiHead = 256;
 
 int dtype_size(int32_t dt) {
     switch (dt) {
@@ -207,8 +209,16 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     const int NT = attn::select_tiles(N);
     p.strips = static_cast<int32_t>((N + 15) / 16);
     p.groups = (p.strips + attn::kWaves - 1) / attn::kWaves;
-    const int64_t units = Hh * p.groups;
-    int64_t wpw = (B * units + kTargetWorkgroups - 1) / kTargetWorkgroups;
+    // several heads per workgroup: 2-byte LDS-DMA path, large windows, no
+    // mask tensor, H a multiple, heads adjacent in the K and V rows
+    p.hpw = (dtype != CRUMPET_DTYPE_F32 && p.vec_io && attn::multi_head_tiles(NT) &&
+             !attn::mask_tensor(kmask) && Hh % attn::kHeadsPerWg == 0 && k_strides[1] == 16 &&
+             v_strides[1] == 16)
+                ? attn::kHeadsPerWg
+                : 1;
+    const int64_t units = Hh / p.hpw * p.groups;
+    const int64_t target = p.hpw > 1 ? kTargetWorkgroupsMultiHead : kTargetWorkgroups;
+    int64_t wpw = (B * units + target - 1) / target;
     if (wpw < 1) wpw = 1;
     p.win_per_wg = static_cast<int32_t>(wpw);
     p.ranges = static_cast<int32_t>((B + wpw - 1) / wpw);

@@ -84,7 +84,33 @@ namespace crumpet {
 namespace attn {
 
 constexpr int kWaves = 4;  // waves (strips) per workgroup
-constexpr int kThreads = 64 * kWaves;
+constexpr int kThreads = 64 * kWaves;  // threads per head slot of a workgroup
+// Heads per workgroup on the LDS-DMA path without a mask tensor, when H is
+// a multiple of it and the heads of a token are adjacent (head stride 16,
+// as in the usual [token][3][H][Dh] qkv layout): the workgroup runs the
+// kWaves strips of each of its heads and stages their K and V together as
+// token records (below), so that its loads read contiguous bytes.  With a
+// mask tensor the heads' waves would all load the same mask rows at once;
+// those launches keep one head per workgroup.
+constexpr int kHeadsPerWg = 3;
+// Tile counts with a kHeadsPerWg variant: the large windows, where K/V
+// staging dominates and 3 heads' double-buffered K/V still fit one CU's LDS.
+constexpr bool multi_head_tiles(int NT) { return NT == 14 || NT == 22; }
+// LDS layout of a kHeadsPerWg workgroup: one record per token with the
+// heads' 16-element rows side by side, as they lie in memory (head stride
+// 16), so that a 1 KB LDS-DMA load covers ~10 tokens' contiguous bytes
+// instead of 32 rows of 32 bytes each.  Record strides in elements: K 56
+// (3 x 16 + 8 of padding: 28 dwords, so 16 lanes reading 16 bytes of 16
+// consecutive rows hit 16 disjoint bank quads), V 48 (24 dwords: the 8 rows
+// of 32 bytes a transpose read touches land on disjoint banks).
+constexpr int kKRec = 56;
+constexpr int kVRec = 48;
+// Rows staged per window (a multiple of 32) and the record regions' sizes in
+// elements: K in whole 1 KB loads of 64 16-byte chunks (7 chunks per token,
+// the seventh a padding load), V in 6-chunk tokens.
+constexpr int rec_rows(int NT) { return (NT * 16 + 31) / 32 * 32; }
+constexpr int rec_k_loads(int NT) { return (rec_rows(NT) * 7 + 63) / 64; }
+constexpr int rec_v_loads(int NT) { return rec_rows(NT) * 6 / 64; }
 constexpr float kLog2e = 1.4426950408889634f;
 // After the first key chunk of a strip, scores may exceed the running row
 // max by this much (natural-log units) before the max is refreshed: the
@@ -94,6 +120,7 @@ constexpr float kLazyMargin = 8.0f;
 
 // Mask modes (template parameter kMask).
 enum MaskKind { kNoMask = 0, kMaskF16 = 1, kMaskF32 = 2, kMaskBF16 = 3, kMaskRegion = 4 };
+constexpr bool mask_tensor(int kind) { return kind != kNoMask && kind != kMaskRegion; }
 
 // Window-type table of region mode: logical window index -> window.
 struct TypeTable {
@@ -123,6 +150,7 @@ struct Params {
     int32_t win_per_wg;      // windows walked by one workgroup
     int32_t ranges;          // ceil(B / win_per_wg)
     int32_t vec_io;          // q/k/v/out rows are 4-element aligned with unit d stride
+    int32_t hpw;             // heads per workgroup: 1, or kHeadsPerWg (H % 3 == 0, LDS-DMA path)
     uint32_t chunks, launched;
     // region mode geometry
     int32_t nWd, nWh, nWw, nW;  // windows per volume along D, H, W and in total
@@ -480,16 +508,16 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 
 // Buffer descriptor words (base, stride 0, num_records, dword-3 flags) for a
-// window's rows, workgroup-uniform.
+// window's rows of `row` elements, workgroup-uniform.
 template <typename T>
-__device__ __forceinline__ u32x4 desc_words(const void* base, int64_t off, int64_t s2, int N) {
+__device__ __forceinline__ u32x4 desc_words(const void* base, int64_t off, int64_t s2, int N, int row = 16) {
     const char* ub = uniform_ptr(static_cast<const char*>(base) + off * int64_t(sizeof(T)));
     const uint64_t a = reinterpret_cast<uint64_t>(ub);
     u32x4 d;
     d[0] = static_cast<uint32_t>(a);
     d[1] = static_cast<uint32_t>(a >> 32) & 0xffffu;
     d[2] = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(
-        static_cast<int>((int64_t(N - 1) * s2 + 16) * int64_t(sizeof(T)))));
+        static_cast<int>((int64_t(N - 1) * s2 + row) * int64_t(sizeof(T)))));
     d[3] = 0x00020000u;
     return d;
 }
@@ -539,8 +567,9 @@ struct Stage<T, NT, true> {
 
     __device__ __forceinline__ void load(const Params& p, int b, int h, int q0, T* k_dst, T* v_dst) {
         const int N = p.N;
-        const int n0 = threadIdx.x >> 2;
-        const int d0 = (threadIdx.x & 3) * 4;
+        const int tid = threadIdx.x & (kThreads - 1);  // within the head slot
+        const int n0 = tid >> 2;
+        const int d0 = (tid & 3) * 4;
         const auto qr = rsrc(p.q, int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1], p.qs[2], N);
         const auto kr = rsrc(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
         const auto vr = rsrc(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
@@ -556,7 +585,7 @@ struct Stage<T, NT, true> {
             // which row half each lane fetches sets the layout (kidx for K,
             // plain rows for V)
             const int lane = threadIdx.x & 63;
-            const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+            const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
             const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
             const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
             typedef __attribute__((address_space(3))) T LdsT;
@@ -585,8 +614,53 @@ struct Stage<T, NT, true> {
         }
     }
 
+    // kHeadsPerWg heads per workgroup: the Q rows of head h as in load(); K
+    // and V of heads h0 .. h0 + kHeadsPerWg - 1 as token records (kKRec /
+    // kVRec elements; the head stride is 16), the 1 KB loads dealt
+    // round-robin to all the workgroup's waves.  Load j of K fills chunks
+    // 64j .. 64j + 63: chunk c is token c / 7, piece c % 7 (piece p < 6 is
+    // bytes 16p .. 16p + 15 of the token's heads, piece 6 pads the record
+    // and reloads piece 0).  The last K load runs past the last record into
+    // the region's padding.
+    __device__ __forceinline__ void load_rec(const Params& p, int b, int h, int h0, int q0, T* k_dst,
+                                             T* v_dst) {
+        static_assert(kDma && kRows == rec_rows(NT), "record staging is an LDS-DMA layout");
+        const int N = p.N;
+        const int tid = threadIdx.x & (kThreads - 1);
+        const int n0 = tid >> 2, d0 = (tid & 3) * 4;
+        constexpr int es = sizeof(T);
+        const auto qr = rsrc(p.q, int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1], p.qs[2], N);
+        rq = ld(qr, (min(q0 + n0, N - 1) * static_cast<int>(p.qs[2]) + d0) * es);
+        const int lane = threadIdx.x & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+        constexpr int kRecElems = 16 * kHeadsPerWg;
+        const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N, kRecElems);
+        const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h0) * p.vs[1], p.vs[2], N, kRecElems);
+        const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
+        typedef __attribute__((address_space(3))) T LdsT;
+        const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
+        const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
+        constexpr int kLoadsK = rec_k_loads(NT), kLoadsV = rec_v_loads(NT);
+        constexpr int kAllWaves = kWaves * kHeadsPerWg;
+        constexpr int kRecRounds = (kLoadsK + kLoadsV + kAllWaves - 1) / kAllWaves;
+#pragma unroll
+        for (int r = 0; r < kRecRounds; ++r) {
+            const int j = wave + kAllWaves * r;  // wave-uniform
+            if (j < kLoadsK) {
+                const int c = 64 * j + lane;
+                const int n = c / 7;
+                const int piece = c - 7 * n;
+                dma16(kd, kl + j * 1024, (min(n, N - 1) * ks2 + (piece == 6 ? 0 : 8 * piece)) * es);
+            } else if (j < kLoadsK + kLoadsV) {
+                const int c = 64 * (j - kLoadsK) + lane;
+                const int n = c / 6;
+                dma16(vd, vl + (j - kLoadsK) * 1024, (min(n, N - 1) * vs2 + 8 * (c - 6 * n)) * es);
+            }
+        }
+    }
+
     __device__ __forceinline__ void store(float scale, T* q_lds, T* k_lds, T* vt_lds) const {
-        const int tid = threadIdx.x;
+        const int tid = threadIdx.x & (kThreads - 1);  // within the head slot
         const int n0 = tid >> 2, d0 = (tid & 3) * 4;
         store_q4<T>(&q_lds[n0 * q_row_elems<T>()], d0, rq, scale);
         if constexpr (!kDma) {
@@ -808,7 +882,7 @@ __device__ __forceinline__ float xmax32(float m) {
 constexpr float kOffsetTarget = 7.0f;     // log2 of the row sum aimed at
 constexpr float kRowSumLimit = 32768.0f;  // row sums (hence every P) stay below 2^15
 
-template <typename T, int NT, int kMask, bool kUseMask, bool kVec>
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec>
 __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
                                               const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
                                               int h, int wave, int qi, int col, int g, float& off) {
@@ -824,10 +898,13 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     const X8 qf = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * 32 + 8 * g]);
 
     // K operand: lane (col, g) reads row col of the tile, dims 8(g&1)..+7
-    const T* kbase = k_lds + (g & 1) * 128 + col * 8;
-    auto kfrag = [&](int t) -> X8 { return *reinterpret_cast<const X8*>(kbase + t * 256); };
+    // (kRec: k_lds and v_lds point at this head's row in the first record)
+    constexpr int kKTile = kRec ? 16 * kKRec : 256;  // elements from one K tile to the next
+    constexpr int kVTile = kRec ? 16 * kVRec : 256;
+    const T* kbase = kRec ? k_lds + col * kKRec + (g & 1) * 8 : k_lds + (g & 1) * 128 + col * 8;
+    auto kfrag = [&](int t) -> X8 { return *reinterpret_cast<const X8*>(kbase + t * kKTile); };
     // V^T fragments by transpose reads of row-major V (lds_read_tr)
-    const T* vrow = &v_lds[(4 * g + (col >> 2)) * 16 + (col & 3) * 4];
+    const T* vrow = &v_lds[(4 * g + (col >> 2)) * (kRec ? kVRec : 16) + (col & 3) * 4];
 
     // Tensor mask through a buffer descriptor spanning exactly the window's
     // [N, N] extent (see attend_f32 for the padding and end-of-extent rules).
@@ -980,8 +1057,8 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             __builtin_amdgcn_sched_barrier(0);
             const int t0 = 2 * pr;
             const bool has1 = t0 + 1 < NT;
-            const X4 v0 = lds_read_tr<T>(vrow + 256 * t0);
-            const X4 v1 = has1 ? lds_read_tr<T>(vrow + 256 * (t0 + 1)) : v0;
+            const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
+            const X4 v1 = has1 ? lds_read_tr<T>(vrow + kVTile * (t0 + 1)) : v0;
 #pragma unroll
             for (int t = t0 + 2 * kKAhead; t < t0 + 2 * kKAhead + 2; ++t)
                 if (t < NT) kf[t] = kfrag(t);
@@ -1024,7 +1101,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             __builtin_amdgcn_sched_barrier(0);
             MaskWords w;
             fetch(t, w);
-            const f32x4 sc = Frag<T>::mma32(lds_load<X8>(ka + t * 512), qf, cinit(t, w));
+            const f32x4 sc = Frag<T>::mma32(lds_load<X8>(ka + t * kKTile * sizeof(T)), qf, cinit(t, w));
             m0 = fmaxf(fmaxf(m0, sc[0]), sc[1]);
             m1 = fmaxf(fmaxf(m1, sc[2]), sc[3]);
             // keeps each tile's max here (pure math may otherwise be sunk
@@ -1047,11 +1124,12 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             MaskWords w0, w1;
             fetch(t0, w0);
             if (has1) fetch(t0 + 1, w1);
-            const f32x4 s0 = Frag<T>::mma32(lds_load<X8>(kb + t0 * 512), qf, cinit(t0, w0) - m);
+            const f32x4 s0 = Frag<T>::mma32(lds_load<X8>(kb + t0 * kKTile * sizeof(T)), qf, cinit(t0, w0) - m);
             f32x4 s1 = s0;
-            if (has1) s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * 512), qf, cinit(t0 + 1, w1) - m);
-            const X4 v0 = lds_read_tr<T>(vrow + 256 * t0);
-            const X4 v1 = has1 ? lds_read_tr<T>(vrow + 256 * (t0 + 1)) : v0;
+            if (has1)
+                s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), qf, cinit(t0 + 1, w1) - m);
+            const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
+            const X4 v1 = has1 ? lds_read_tr<T>(vrow + kVTile * (t0 + 1)) : v0;
             accumulate(probs(s0, s1, has1), v0, v1, has1, o, lacc);
             // keeps the O product in this iteration (it would otherwise be
             // sunk towards the store, keeping every V fragment live)
@@ -1269,25 +1347,41 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
     }
 }
 
-template <typename T, int NT, int kMask, bool kVec>
-__global__ void __launch_bounds__(kThreads)
+// HPW heads per workgroup (1, or kHeadsPerWg on the LDS-DMA path): head slot
+// s = threadIdx.x / kThreads runs the kWaves strips of head h0 + s with its
+// own K/V buffers; the slots share the window walk and the barriers.
+template <typename T, int NT, int kMask, bool kVec, int HPW>
+__global__ void __launch_bounds__(kThreads * HPW)
 __attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask, kVec>(), waves_per_eu<T, NT, kMask, kVec>())))
 swin_attention_d16_kernel(const Params p) {
     typedef Stage<T, NT, kVec> St;
     constexpr int NP = St::NP;
-    __shared__ __attribute__((aligned(16))) T q_lds[2][St::kQRows * q_row_elems<T>()];
-    __shared__ __attribute__((aligned(16))) T k_lds[2][St::kRows * 16];
-    __shared__ __attribute__((aligned(16))) T vt_lds[2][St::kVLds];
+    // Q rows are wave-private on the LDS-DMA path (a wave stores and reads
+    // only its own 16 rows, in that order), so one buffer serves there.
+    constexpr int kQBufs = HPW > 1 ? 1 : 2;
+    static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
+    constexpr bool kRecs = HPW > 1;  // token-record K/V layout shared by the head slots
+    constexpr int kKLds = kRecs ? rec_k_loads(NT) * 512 : St::kRows * 16;
+    constexpr int kVLdsAll = kRecs ? rec_rows(NT) * kVRec : St::kVLds;
+    __shared__ __attribute__((aligned(16))) T q_lds[kQBufs][HPW][St::kQRows * q_row_elems<T>()];
+    __shared__ __attribute__((aligned(16))) T k_lds[2][kKLds];
+    __shared__ __attribute__((aligned(16))) T vt_lds[2][kVLdsAll];
     __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
+    static_assert(sizeof(q_lds) + sizeof(k_lds) + sizeof(vt_lds) + sizeof(cls_lds) <= 160 * 1024,
+                  "LDS footprint exceeds the 160 KB of a gfx950 CU");
 
     uint32_t chunk;
     if (!xcd_chunk(blockIdx.x, p.launched, p.chunks, chunk)) return;
-    // chunk = (range * H + h) * groups + group: the groups of one (range, head)
-    // are consecutive, hence on one XCD, and share its L2 for K/V.
+    // chunk = (range * (H / HPW) + head block) * groups + group: the groups of
+    // one (range, head block) are consecutive, hence on one XCD, and share
+    // its L2 for K/V.
+    const int slot = HPW > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kThreads) : 0;
+    const int hb_count = p.H / HPW;
     const int grp = static_cast<int>(chunk % p.groups);
     const int rh = static_cast<int>(chunk / p.groups);
-    const int h = rh % p.H;
-    const int range = rh / p.H;
+    const int h0 = (rh % hb_count) * HPW;  // first head of the workgroup
+    const int h = h0 + slot;
+    const int range = rh / hb_count;
     // Tensor-mask modes take every ranges-th window (range, range + ranges,
     // ...): a window whose boundary flag is set costs more than one whose
     // flag is clear, and boundary windows come in runs (the last window
@@ -1298,7 +1392,7 @@ swin_attention_d16_kernel(const Params p) {
     const int i1 = kStrided ? (p.B - range + p.ranges - 1) / p.ranges : min(p.B, i0 + p.win_per_wg);
 
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = HPW > 1 ? (threadIdx.x >> 6) & (kWaves - 1) : threadIdx.x >> 6;  // strip within the group
     const int col = lane & 15;
     const int g = lane >> 4;
     const int strip = grp * kWaves + wave;
@@ -1309,7 +1403,7 @@ swin_attention_d16_kernel(const Params p) {
     if constexpr (kMask == kMaskRegion) {
         // shift-region class of every window token: one bit per axis, set at
         // or past ws - ss (covered by the prologue barrier below)
-        for (int j = threadIdx.x; j < NP; j += kThreads) {
+        for (int j = threadIdx.x; j < NP; j += kThreads * HPW) {
             int c = 0;
             if (j < p.N) {
                 const int lw = j % p.ws[2];
@@ -1343,8 +1437,14 @@ swin_attention_d16_kernel(const Params p) {
     bool flag_next = true;
     if constexpr (kMask != kNoMask && kMask != kMaskRegion)
         flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
-    st.load(p, b_next, h, q0, k_lds[0], vt_lds[0]);
-    st.store(qscale, q_lds[0], k_lds[0], vt_lds[0]);
+    auto stage_load = [&](int bw, int sb) {
+        if constexpr (kRecs)
+            st.load_rec(p, bw, h, h0, q0, k_lds[sb], vt_lds[sb]);
+        else
+            st.load(p, bw, h, q0, k_lds[sb], vt_lds[sb]);
+    };
+    stage_load(b_next, 0);
+    st.store(qscale, q_lds[0][slot], k_lds[0], vt_lds[0]);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
     __syncthreads();
 
@@ -1368,29 +1468,32 @@ swin_attention_d16_kernel(const Params p) {
             b_next = it.window(p, code_next);
             if constexpr (kMask != kNoMask && kMask != kMaskRegion)
                 flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
-            st.load(p, b_next, h, q0, k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+            stage_load(b_next, buf ^ 1);
         }
+        const int qb = kQBufs == 2 ? buf : 0;
+        T* const qw = q_lds[qb][slot];
+        T* const kw = k_lds[buf] + (kRecs ? 16 * slot : 0);  // this head's row of each record
+        T* const vw = vt_lds[buf] + (kRecs ? 16 * slot : 0);
         if (active) {
             constexpr bool kTensor = kMask != kNoMask && kMask != kMaskRegion;
             bool use_mask = false;
             if constexpr (kTensor) use_mask = flag;
             if constexpr (sizeof(T) == 2) {
                 if (use_mask)
-                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec>(p, bs, q_lds[buf], k_lds[buf],
-                                                                         vt_lds[buf], b, h, wave, qi, col, g, off);
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs>(p, bs, qw, kw, vw, b, h, wave, qi,
+                                                                         col, g, off);
                 else
-                    rebuild = attend_offset<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf],
-                                                                       vt_lds[buf], b, h, wave, qi, col, g, off);
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs>(p, bs, qw, kw, vw, b, h, wave, qi,
+                                                                       col, g, off);
             } else {
                 if (use_mask)
-                    attend_f32<T, NT, kMask, kTensor, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h,
-                                                            wave, qi, col, g);
+                    attend_f32<T, NT, kMask, kTensor, kVec>(p, bs, qw, kw, vw, b, h, wave, qi, col, g);
                 else
-                    attend_f32<T, NT, kMask, false, kVec>(p, bs, q_lds[buf], k_lds[buf], vt_lds[buf], b, h,
-                                                          wave, qi, col, g);
+                    attend_f32<T, NT, kMask, false, kVec>(p, bs, qw, kw, vw, b, h, wave, qi, col, g);
             }
         }
-        if (i + 1 < i1) st.store(qscale, q_lds[buf ^ 1], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+        if (i + 1 < i1)
+            st.store(qscale, q_lds[kQBufs == 2 ? buf ^ 1 : 0][slot], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
         __syncthreads();
     }
@@ -1399,15 +1502,21 @@ swin_attention_d16_kernel(const Params p) {
 // Launch for element type T; NT from kTileCounts, kmask a MaskKind.
 template <typename T>
 void launch(const Params& p, int NT, int kmask, hipStream_t s) {
-    const dim3 grid(p.launched), block(kThreads);
-#define CRUMPET_ATTN_MASK(NTV, MK)                                                              \
-    do {                                                                                        \
-        if (p.vec_io)                                                                           \
-            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true>), grid, block, 0, s,  \
-                               p);                                                              \
-        else                                                                                    \
-            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, false>), grid, block, 0, s, \
-                               p);                                                              \
+    const dim3 grid(p.launched), block(kThreads * p.hpw);
+#define CRUMPET_ATTN_MASK(NTV, MK)                                                                    \
+    do {                                                                                              \
+        if (p.vec_io) {                                                                               \
+            if constexpr (v_row_major<T>() && multi_head_tiles(NTV) && !mask_tensor(MK)) {            \
+                if (p.hpw == kHeadsPerWg) {                                                           \
+                    hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true, kHeadsPerWg>), grid, \
+                                       block, 0, s, p);                                               \
+                    break;                                                                            \
+                }                                                                                     \
+            }                                                                                         \
+            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true, 1>), grid, block, 0, s, p); \
+        } else {                                                                                      \
+            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, false, 1>), grid, block, 0, s, p); \
+        }                                                                                             \
     } while (0)
 #define CRUMPET_ATTN_NT(NTV)                                            \
     case NTV:                                                           \

@@ -328,3 +328,62 @@ def test_tile_count_boundaries(oracle, dev, N, dtype):
                                None if mask is None else mask.to(dev), None if bnd is None else bnd.to(dev),
                                scale=0.25)
     _compare(out, ref, dtype, f"N={N} {dtype}")
+
+
+def _interleaved(B, N, H, dtype, seed):
+    """q, k, v as views of one [B, N, 3, H, Dh] qkv tensor (the MONAI layout:
+    a token's heads adjacent, head stride 16), plus the CPU tensor."""
+    qkv = seeded((B, N, 3 * H * 16), dtype, seed)
+    return qkv, qkv.reshape(B, N, 3, H, 16).permute(2, 0, 3, 1, 4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("H", [3, 6])
+@pytest.mark.parametrize("ws", [(6, 6, 6), (7, 7, 7)])
+@pytest.mark.parametrize("shifted", [True, False], ids=["region", "nomask"])
+def test_head_records_interleaved_qkv(oracle, dev, dtype, H, ws, shifted):
+    """Interleaved qkv with H a multiple of 3 runs three heads per workgroup
+    with K/V staged as token records (N = 216 and 343: both tile counts that
+    have that variant); every window against the oracle, and against the
+    same data in separate contiguous tensors (one head per workgroup)."""
+    from crumpet_amd.fused_attention import fused_swin_attention_shifted
+
+    vol = tuple(2 * w for w in ws)
+    ss = tuple(w // 2 for w in ws) if shifted else (0, 0, 0)
+    N = ws[0] * ws[1] * ws[2]
+    B = 8 * 2  # two outer batches of 8 windows
+    qkv, t = _interleaved(B, N, H, dtype, 1300 + N + H)
+    rows = (2 * ws[0] - 1) * (2 * ws[1] - 1) * (2 * ws[2] - 1)
+    bias = bias_from_table(trunc_normal_table(rows, H, 1301 + H), ws).to(dtype)
+    m = oracle.attn_mask(*vol, ws, ss, "float32") if shifted else None
+    ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), None if m is None else m[np.arange(B) % 8],
+                           None, scale=0.25)
+    td = qkv.to(dev).reshape(B, N, 3, H, 16).permute(2, 0, 3, 1, 4)
+    out_bnc = torch.empty((B, N, H * 16), dtype=dtype, device=dev)
+    out = out_bnc.view(B, N, H, 16).permute(0, 2, 1, 3)
+    if shifted:
+        fused_swin_attention_shifted(td[0], td[1], td[2], bias.to(dev), vol, ws, ss, scale=0.25, out=out)
+    else:
+        fused_swin_attention(td[0], td[1], td[2], bias.to(dev), None, scale=0.25, out=out)
+    _compare(out, ref, dtype, f"records H={H} N={N} {'region' if shifted else 'nomask'}")
+    sep = [x.contiguous() for x in td]
+    if shifted:
+        other = fused_swin_attention_shifted(sep[0], sep[1], sep[2], bias.to(dev), vol, ws, ss, scale=0.25)
+    else:
+        other = fused_swin_attention(sep[0], sep[1], sep[2], bias.to(dev), None, scale=0.25)
+    diff = (out.float() - other.float()).abs().max().item()
+    assert diff <= TOL[dtype], diff
+
+
+@pytest.mark.parametrize("N", [209, 224, 337, 352])
+def test_head_records_tile_edges(oracle, dev, N):
+    """The record path at the smallest and largest N of its tile counts (14
+    and 22), any N, no mask: padded key rows of the records repeat row N-1
+    and are masked by the bias tiles."""
+    dtype, H, B = torch.float16, 3, 5
+    qkv, t = _interleaved(B, N, H, dtype, 1400 + N)
+    bias = seeded((H, N, N), torch.float32, 1401 + N)
+    ref = oracle.attention(_f32(t[0]), _f32(t[1]), _f32(t[2]), _f32(bias), None, None, scale=0.25)
+    td = qkv.to(dev).reshape(B, N, 3, H, 16).permute(2, 0, 3, 1, 4)
+    out = fused_swin_attention(td[0], td[1], td[2], bias.to(dev), None, scale=0.25)
+    _compare(out, ref, dtype, f"records N={N}")
