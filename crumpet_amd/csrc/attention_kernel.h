@@ -76,6 +76,7 @@
 #include <hip/hip_runtime.h>
 
 #include <math.h>
+#include <type_traits>
 
 #include "crumpet_common.h"
 #include "crumpet_hip.h"
@@ -96,21 +97,24 @@ constexpr int kHeadsPerWg = 3;
 // Tile counts with a kHeadsPerWg variant: the large windows, where K/V
 // staging dominates and 3 heads' double-buffered K/V still fit one CU's LDS.
 constexpr bool multi_head_tiles(int NT) { return NT == 14 || NT == 22; }
-// LDS layout of a kHeadsPerWg workgroup: one record per token with the
-// heads' 16-element rows side by side, as they lie in memory (head stride
-// 16), so that a 1 KB LDS-DMA load covers ~10 tokens' contiguous bytes
-// instead of 32 rows of 32 bytes each.  Record strides in elements: K 56
-// (3 x 16 + 8 of padding: 28 dwords, so 16 lanes reading 16 bytes of 16
-// consecutive rows hit 16 disjoint bank quads), V 48 (24 dwords: the 8 rows
-// of 32 bytes a transpose read touches land on disjoint banks).
-constexpr int kKRec = 56;
-constexpr int kVRec = 48;
-// Rows staged per window (a multiple of 32) and the record regions' sizes in
-// elements: K in whole 1 KB loads of 64 16-byte chunks (7 chunks per token,
-// the seventh a padding load), V in 6-chunk tokens.
+// LDS layout of a kHeadsPerWg workgroup: one record per token holding the
+// K rows of its heads, then their V rows, as they lie in memory (head
+// stride 16, V a fixed distance after K with the same strides), so that a
+// 1 KB LDS-DMA load reads ~5 tokens' contiguous K+V bytes.  A vector load
+// moves whole 128-byte lines from L2 at a fixed rate per CU, and K+V of a
+// token is 2.25 lines; separate 32-byte rows would cost one line each.
+// Record stride 104 elements (K 48, V 48, 8 of padding): 52 dwords, so the
+// 16 lanes of a K fragment read (16 bytes of 16 consecutive rows) and the
+// 4 rows of 32 bytes a 16-lane group of a V transpose read touches land on
+// disjoint banks.
+constexpr int kRecStride = 104;
+constexpr int kRecV = 48;  // V rows' offset in a record
+constexpr int kKRec = kRecStride;
+constexpr int kVRec = kRecStride;
+// Rows staged per window (a multiple of 32) and the loads of a window: 13
+// 16-byte chunks per token (6 of K, 6 of V, a padding load), 64 per load.
 constexpr int rec_rows(int NT) { return (NT * 16 + 31) / 32 * 32; }
-constexpr int rec_k_loads(int NT) { return (rec_rows(NT) * 7 + 63) / 64; }
-constexpr int rec_v_loads(int NT) { return rec_rows(NT) * 6 / 64; }
+constexpr int rec_loads(int NT) { return (rec_rows(NT) * 13 + 63) / 64; }
 constexpr float kLog2e = 1.4426950408889634f;
 // After the first key chunk of a strip, scores may exceed the running row
 // max by this much (natural-log units) before the max is refreshed: the
@@ -151,6 +155,7 @@ struct Params {
     int32_t ranges;          // ceil(B / win_per_wg)
     int32_t vec_io;          // q/k/v/out rows are 4-element aligned with unit d stride
     int32_t hpw;             // heads per workgroup: 1, or kHeadsPerWg (H % 3 == 0, LDS-DMA path)
+    int32_t kv_delta;        // hpw > 1: elements from a K row to the V row of the same token and head
     uint32_t chunks, launched;
     // region mode geometry
     int32_t nWd, nWh, nWw, nW;  // windows per volume along D, H, W and in total
@@ -579,31 +584,8 @@ struct Stage<T, NT, true> {
         const int nq = min(q0 + n0, N - 1);
         rq = ld(qr, (nq * qs2 + d0) * es);
         if constexpr (kDma) {
-            // 16 bytes per lane straight into LDS: the 64 lanes of wave w in
-            // round r fill the 1 KB of rows 32*(4r + w) .. +31 at a
-            // wave-uniform LDS address, lane l writing its 16-byte chunk l;
-            // which row half each lane fetches sets the layout (kidx for K,
-            // plain rows for V)
-            const int lane = threadIdx.x & 63;
-            const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
-            const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
-            const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
-            typedef __attribute__((address_space(3))) T LdsT;
-            const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
-            const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
 #pragma unroll
-            for (int r = 0; r < kRounds; ++r) {
-                const int row0 = 32 * (4 * r + wave);
-                if (row0 < kRows) {  // wave-uniform
-                    // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15)
-                    const int nk = min(row0 + ((lane >> 5) << 4) + (lane & 15), N - 1);
-                    const int hk = ((lane >> 4) & 1) * 8;
-                    dma16(kd, kl + row0 * 32, (nk * ks2 + hk) * es);
-                    // V: plain 32-byte rows (its transpose reads are conflict-free)
-                    const int nv = min(row0 + (lane >> 1), N - 1);
-                    dma16(vd, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
-                }
-            }
+            for (int r = 0; r < kRounds; ++r) dma_round<false>(p, b, h, h, k_dst, v_dst, r);
         } else {
 #pragma unroll
             for (int k = 0; k < kKC; ++k) {
@@ -614,47 +596,78 @@ struct Stage<T, NT, true> {
         }
     }
 
-    // kHeadsPerWg heads per workgroup: the Q rows of head h as in load(); K
-    // and V of heads h0 .. h0 + kHeadsPerWg - 1 as token records (kKRec /
-    // kVRec elements; the head stride is 16), the 1 KB loads dealt
-    // round-robin to all the workgroup's waves.  Load j of K fills chunks
-    // 64j .. 64j + 63: chunk c is token c / 7, piece c % 7 (piece p < 6 is
-    // bytes 16p .. 16p + 15 of the token's heads, piece 6 pads the record
-    // and reloads piece 0).  The last K load runs past the last record into
-    // the region's padding.
-    __device__ __forceinline__ void load_rec(const Params& p, int b, int h, int h0, int q0, T* k_dst,
-                                             T* v_dst) {
-        static_assert(kDma && kRows == rec_rows(NT), "record staging is an LDS-DMA layout");
+    // The Q rows of head h for the next window (the register half of load()).
+    __device__ __forceinline__ void load_q(const Params& p, int b, int h, int q0) {
         const int N = p.N;
         const int tid = threadIdx.x & (kThreads - 1);
         const int n0 = tid >> 2, d0 = (tid & 3) * 4;
         constexpr int es = sizeof(T);
         const auto qr = rsrc(p.q, int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1], p.qs[2], N);
         rq = ld(qr, (min(q0 + n0, N - 1) * static_cast<int>(p.qs[2]) + d0) * es);
+    }
+
+    // LDS-DMA rounds per wave for one window's K and V: kRounds with one
+    // head per workgroup, one record load per round with kHeadsPerWg heads.
+    template <bool kRecs>
+    static constexpr int dma_rounds() {
+        constexpr int kAllWaves = kWaves * kHeadsPerWg;
+        return kRecs ? (rec_loads(NT) + kAllWaves - 1) / kAllWaves : kRounds;
+    }
+
+    // Round r of this wave's LDS-DMA loads of window b's K and V.  16 bytes
+    // per lane go straight into LDS at a wave-uniform address, lane l
+    // writing 16-byte chunk l of the load's 1 KB; which bytes each lane
+    // fetches sets the layout.
+    //  - One head (h): round r of wave w fills rows 32*(4r + w) .. +31, K in
+    //    the kidx tile layout, V as plain 32-byte rows (its transpose reads
+    //    are conflict-free).
+    //  - kHeadsPerWg heads (h0 ..): token records (kRecStride elements),
+    //    load j = wave + 4 * kHeadsPerWg * r of the workgroup's loads fills
+    //    chunks 64j .. 64j + 63: chunk c is token c / 13, piece c % 13 (pieces
+    //    0-5: the heads' K row bytes 16p .. 16p + 15, pieces 6-11 the same of
+    //    V, which lies p.kv_delta elements after K; piece 12 pads the record
+    //    and reloads piece 0).  The last load may run past the last record
+    //    into the buffer's padding.
+    template <bool kRecs>
+    static __device__ __forceinline__ void dma_round(const Params& p, int b, int h, int h0, T* k_dst, T* v_dst,
+                                                     int r) {
+        static_assert(kDma, "LDS-DMA staging");
+        const int N = p.N;
+        constexpr int es = sizeof(T);
         const int lane = threadIdx.x & 63;
-        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
-        constexpr int kRecElems = 16 * kHeadsPerWg;
-        const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N, kRecElems);
-        const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h0) * p.vs[1], p.vs[2], N, kRecElems);
         const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
         typedef __attribute__((address_space(3))) T LdsT;
         const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
         const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
-        constexpr int kLoadsK = rec_k_loads(NT), kLoadsV = rec_v_loads(NT);
-        constexpr int kAllWaves = kWaves * kHeadsPerWg;
-        constexpr int kRecRounds = (kLoadsK + kLoadsV + kAllWaves - 1) / kAllWaves;
-#pragma unroll
-        for (int r = 0; r < kRecRounds; ++r) {
-            const int j = wave + kAllWaves * r;  // wave-uniform
-            if (j < kLoadsK) {
+        if constexpr (!kRecs) {
+            const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
+            const int row0 = 32 * (4 * r + wave);
+            if (row0 < kRows) {  // wave-uniform
+                const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
+                const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
+                // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15)
+                const int nk = min(row0 + ((lane >> 5) << 4) + (lane & 15), N - 1);
+                const int hk = ((lane >> 4) & 1) * 8;
+                dma16(kd, kl + row0 * 32, (nk * ks2 + hk) * es);
+                const int nv = min(row0 + (lane >> 1), N - 1);
+                dma16(vd, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
+            }
+        } else {
+            static_assert(kRows == rec_rows(NT), "record rows");
+            (void)v_dst;
+            (void)vl;
+            (void)vs2;
+            const int kvd = p.kv_delta;
+            const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+            const int j = wave + kWaves * kHeadsPerWg * r;  // wave-uniform
+            if (j < rec_loads(NT)) {
+                const u32x4 d = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N,
+                                              kvd + 16 * kHeadsPerWg);
                 const int c = 64 * j + lane;
-                const int n = c / 7;
-                const int piece = c - 7 * n;
-                dma16(kd, kl + j * 1024, (min(n, N - 1) * ks2 + (piece == 6 ? 0 : 8 * piece)) * es);
-            } else if (j < kLoadsK + kLoadsV) {
-                const int c = 64 * (j - kLoadsK) + lane;
-                const int n = c / 6;
-                dma16(vd, vl + (j - kLoadsK) * 1024, (min(n, N - 1) * vs2 + 8 * (c - 6 * n)) * es);
+                const int n = c / 13;
+                const int piece = c - 13 * n;
+                const int part = piece < 6 ? 8 * piece : (piece < 12 ? kvd + 8 * (piece - 6) : 0);
+                dma16(d, kl + j * 1024, (min(n, N - 1) * ks2 + part) * es);
             }
         }
     }
@@ -882,10 +895,32 @@ __device__ __forceinline__ float xmax32(float m) {
 constexpr float kOffsetTarget = 7.0f;     // log2 of the row sum aimed at
 constexpr float kRowSumLimit = 32768.0f;  // row sums (hence every P) stay below 2^15
 
-template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec>
+// The next window's LDS-DMA rounds, issued from inside a window's compute:
+// attend_offset spreads them over its tile pairs, so that a workgroup's
+// loads reach the memory pipeline a few at a time while it computes instead
+// of all at the window start (where every wave would stall on issue).
+template <typename T, typename St, bool kRecs>
+struct DmaIssuer {
+    static constexpr int kRounds = St::template dma_rounds<kRecs>();
+    const Params* p;
+    int b, h, h0;
+    T* k_dst;
+    T* v_dst;
+    bool on;  // a next window exists (wave-uniform)
+    __device__ __forceinline__ void operator()(int r) const {
+        if (on) St::template dma_round<kRecs>(*p, b, h, h0, k_dst, v_dst, r);
+    }
+};
+struct NoIssue {
+    static constexpr int kRounds = 0;
+    __device__ __forceinline__ void operator()(int) const {}
+};
+
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, typename Issue>
 __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
                                               const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
-                                              int h, int wave, int qi, int col, int g, float& off) {
+                                              int h, int wave, int qi, int col, int g, float& off,
+                                              const Issue& issue) {
     typedef typename Frag<T>::x4 X4;
     typedef typename Frag<T>::x8 X8;
     constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
@@ -1055,6 +1090,11 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
 #pragma unroll
         for (int pr = 0; pr < kPairs; ++pr) {
             __builtin_amdgcn_sched_barrier(0);
+            // the next window's DMA rounds ceil(pr R / P) .. ceil((pr+1) R / P) - 1
+#pragma unroll
+            for (int k = (pr * Issue::kRounds + kPairs - 1) / kPairs;
+                 k < ((pr + 1) * Issue::kRounds + kPairs - 1) / kPairs; ++k)
+                issue(k);
             const int t0 = 2 * pr;
             const bool has1 = t0 + 1 < NT;
             const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
@@ -1361,8 +1401,10 @@ swin_attention_d16_kernel(const Params p) {
     constexpr int kQBufs = HPW > 1 ? 1 : 2;
     static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
     constexpr bool kRecs = HPW > 1;  // token-record K/V layout shared by the head slots
-    constexpr int kKLds = kRecs ? rec_k_loads(NT) * 512 : St::kRows * 16;
-    constexpr int kVLdsAll = kRecs ? rec_rows(NT) * kVRec : St::kVLds;
+    // (kRecs: K and V in one record array, k_lds; the last load's spill
+    // lands in its padding)
+    constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * 16;
+    constexpr int kVLdsAll = kRecs ? 8 : St::kVLds;
     __shared__ __attribute__((aligned(16))) T q_lds[kQBufs][HPW][St::kQRows * q_row_elems<T>()];
     __shared__ __attribute__((aligned(16))) T k_lds[2][kKLds];
     __shared__ __attribute__((aligned(16))) T vt_lds[2][kVLdsAll];
@@ -1437,11 +1479,19 @@ swin_attention_d16_kernel(const Params p) {
     bool flag_next = true;
     if constexpr (kMask != kNoMask && kMask != kMaskRegion)
         flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
+    // 2-byte LDS-DMA staging: the Q rows by register, K and V in DMA rounds
+    // (all at once here and for waves without a strip, spread over the
+    // compute of the previous window otherwise)
+    constexpr bool kSpread = kVec && v_row_major<T>();  // Stage<T, NT, true>::kDma
     auto stage_load = [&](int bw, int sb) {
-        if constexpr (kRecs)
-            st.load_rec(p, bw, h, h0, q0, k_lds[sb], vt_lds[sb]);
-        else
+        if constexpr (kSpread) {
+            st.load_q(p, bw, h, q0);
+#pragma unroll
+            for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r)
+                St::template dma_round<kRecs>(p, bw, h, h0, k_lds[sb], vt_lds[sb], r);
+        } else {
             st.load(p, bw, h, q0, k_lds[sb], vt_lds[sb]);
+        }
     };
     stage_load(b_next, 0);
     st.store(qscale, q_lds[0][slot], k_lds[0], vt_lds[0]);
@@ -1468,23 +1518,37 @@ swin_attention_d16_kernel(const Params p) {
             b_next = it.window(p, code_next);
             if constexpr (kMask != kNoMask && kMask != kMaskRegion)
                 flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
-            stage_load(b_next, buf ^ 1);
+            if constexpr (kSpread) {
+                if (active)
+                    st.load_q(p, b_next, h, q0);
+                else
+                    stage_load(b_next, buf ^ 1);
+            } else {
+                stage_load(b_next, buf ^ 1);
+            }
         }
+        const auto issue = [&]() {
+            if constexpr (kSpread)
+                return DmaIssuer<T, St, kRecs>{&p, b_next, h, h0, k_lds[buf ^ 1], vt_lds[buf ^ 1], i + 1 < i1};
+            else
+                return NoIssue{};
+        }();
+        typedef std::decay_t<decltype(issue)> Issuer;
         const int qb = kQBufs == 2 ? buf : 0;
         T* const qw = q_lds[qb][slot];
-        T* const kw = k_lds[buf] + (kRecs ? 16 * slot : 0);  // this head's row of each record
-        T* const vw = vt_lds[buf] + (kRecs ? 16 * slot : 0);
+        T* const kw = k_lds[buf] + (kRecs ? 16 * slot : 0);  // this head's rows of each record
+        T* const vw = kRecs ? k_lds[buf] + kRecV + 16 * slot : vt_lds[buf];
         if (active) {
             constexpr bool kTensor = kMask != kNoMask && kMask != kMaskRegion;
             bool use_mask = false;
             if constexpr (kTensor) use_mask = flag;
             if constexpr (sizeof(T) == 2) {
                 if (use_mask)
-                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs>(p, bs, qw, kw, vw, b, h, wave, qi,
-                                                                         col, g, off);
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, Issuer>(
+                        p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
                 else
-                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs>(p, bs, qw, kw, vw, b, h, wave, qi,
-                                                                       col, g, off);
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, Issuer>(
+                        p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
             } else {
                 if (use_mask)
                     attend_f32<T, NT, kMask, kTensor, kVec>(p, bs, qw, kw, vw, b, h, wave, qi, col, g);
