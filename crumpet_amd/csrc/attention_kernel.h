@@ -187,6 +187,26 @@ inline int select_tiles(int64_t N) {
     return -1;
 }
 
+// The first tile that can hold key N - 1 for an N that selects NT tiles
+// (N > 16 * the previous tile count).
+constexpr int first_last_tile(int NT) {
+    int prev = 0;
+    for (int c : kTileCounts) {
+        if (c == NT) return prev;
+        prev = c;
+    }
+    return 0;
+}
+
+// Buffer loads are range-checked per dword: on row N - 1 of an [N, N]
+// extent of 16-bit values that ends in the middle of a dword, the dword
+// holding key N - 1 reads 0.  The lane whose 4 keys 16t + 4g .. + 3 of row
+// N - 1 include key N - 1 reads them element by element instead.
+template <int NT>
+__device__ __forceinline__ bool holds_last_key(int t, int row, int g, int N) {
+    return t >= first_last_tile(NT) && row == N - 1 && 16 * t + 4 * g <= N - 1 && 16 * t + 4 * g + 3 >= N - 1;
+}
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -755,16 +775,13 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
                 for (int i = 0; i < 3; ++i) raw[u][i] = w[i];
             }
         }
-        constexpr int tl = NT - 1;
-        if (tl >= t0 && tl < t0 + kHalf && qr == N - 1 && 16 * tl + 4 * g + 3 >= N) {
-            // the end-of-extent tile, element by element, laid out as the
-            // vector load would have returned it
-            const int u = tl - t0;
-            if constexpr (kEs == 4) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    raw[u][r] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff + kTileBytes * tl + 4 * r, 0, 0);
-            } else {
+        for (int u = 0; u < kHalf; ++u) {
+            const int tl = t0 + u;
+            if (kEs == 4 || tl >= NT || !holds_last_key<NT>(tl, qr, g, N)) continue;
+            // the tile holding the last key of the last row (16-bit), element
+            // by element, laid out as the vector load would have returned it
+            {
                 uint32_t kv[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -979,11 +996,9 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) w[r] = v4[r];
             }
-            if (t == NT - 1 && qi == N - 1 && 16 * t + 4 * g + 3 >= N) {
-                // this load reaches past the extent end, where a range check
-                // at dword granularity could zero in-range keys: read the 4
-                // keys element by element and lay them out as the three
-                // dwords would hold them
+            if (kMaskBytes == 2 && holds_last_key<NT>(t, qi, g, N)) {
+                // 16-bit keys of the last row holding key N - 1: element by
+                // element, laid out as the three dwords would hold them
                 if constexpr (kMaskBytes == 2) {
                     uint32_t kv[4];
 #pragma unroll
@@ -1256,9 +1271,9 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
 #pragma unroll
                 for (int r = 0; r < 4; ++r) mq[4 * slot + r] = w[r];
             }
-            // the load that reaches past the extent end (row N-1, last tile)
-            // is read again element by element (compile-time tile test)
-            if (t == NT - 1 && qi == N - 1 && 16 * t + 4 * g + 3 >= N) {
+            // the 16-bit keys of the last row holding key N - 1 are read again
+            // element by element
+            if (kMaskBytes == 2 && holds_last_key<NT>(t, qi, g, N)) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if constexpr (kMaskBytes == 2) {

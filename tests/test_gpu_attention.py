@@ -387,3 +387,23 @@ def test_head_records_tile_edges(oracle, dev, N):
     td = qkv.to(dev).reshape(B, N, 3, H, 16).permute(2, 0, 3, 1, 4)
     out = fused_swin_attention(td[0], td[1], td[2], bias.to(dev), None, scale=0.25)
     _compare(out, ref, dtype, f"records N={N}")
+
+
+@pytest.mark.parametrize("N", [129, 131, 225, 353])
+@pytest.mark.parametrize("dt16", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_last_key_of_last_row_16bit(oracle, dev, N, dt16):
+    """16-bit bias and mask whose [N, N] extent ends in the middle of a dword,
+    at N where the tile count is rounded up (key N-1 is not in the last
+    tile): the last row's last key must keep its bias and mask values (a
+    dword-granular range check would read them as 0)."""
+    dtype, H, B = torch.float16, 2, 3
+    q, k, v = _inputs(B, H, N, 16, dtype, 1500 + N)
+    bias = (seeded((H, N, N), torch.float32, 1501 + N) * 0.5).to(dt16)
+    bias[:, N - 1, N - 1] = 4.0  # a large bias on the last key of the last row
+    mask = torch.where(seeded((B, N, N), torch.float32, 1502 + N) > 0.5, -100.0, 0.0).to(dt16)
+    mask[:, N - 1, :] = 0.0
+    mask[0, N - 1, N - 1] = -100.0  # window 0: the last key of the last row masked
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), None, scale=0.25)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), None, scale=0.25)
+    _compare(out, ref, dtype, f"N={N} {dt16} last key")
+    _compare(out[:, :, N - 1], ref[:, :, N - 1], dtype, f"N={N} {dt16} last row")
