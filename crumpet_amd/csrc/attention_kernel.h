@@ -198,13 +198,36 @@ constexpr int first_last_tile(int NT) {
     return 0;
 }
 
-// Buffer loads are range-checked per dword: on row N - 1 of an [N, N]
-// extent of 16-bit values that ends in the middle of a dword, the dword
-// holding key N - 1 reads 0.  The lane whose 4 keys 16t + 4g .. + 3 of row
-// N - 1 include key N - 1 reads them element by element instead.
-template <int NT>
-__device__ __forceinline__ bool holds_last_key(int t, int row, int g, int N) {
-    return t >= first_last_tile(NT) && row == N - 1 && 16 * t + 4 * g <= N - 1 && 16 * t + 4 * g + 3 >= N - 1;
+// Whether lane keys k0 .. k0 + nk - 1 of row `row` include key N - 1 of row
+// N - 1 (the fp32-operand kernel's mask reads those element by element).
+__device__ __forceinline__ bool holds_last_key(int k0, int nk, int row, int N) {
+    return row == N - 1 && k0 <= N - 1 && k0 + nk - 1 >= N - 1;
+}
+
+// Key order.  Tile t's row 4g + r (lane group g's key r of the tile) holds
+// key 16t + 4g + r, except in the paired order (kPaired): in each full pair
+// of tiles (2p, 2p + 1), row 4g + r of tile 2p + j holds key 32p + 8g +
+// 4j + r, so that the 8 keys a lane holds across the pair are consecutive
+// (one load of its mask or bias values per pair instead of two, over half
+// the cache lines).  A lone last tile keeps the plain order.  Attention
+// sums over keys: K, V, the bias and the mask only have to agree on the
+// order.
+template <int NT, bool kPaired>
+__device__ __forceinline__ int key_of(int u) {  // u = 16t + 4g + r, any lane slot or LDS row
+    const int t = u >> 4;
+    if (!kPaired || u >= 16 * NT || (t | 1) >= NT) return u;
+    const int i = u & 15;
+    return (u & ~31) + ((i >> 2) << 3) + ((t & 1) << 2) + (i & 3);
+}
+// Keys per lane in the load unit starting at tile t0 (4, or 8 for a full
+// pair in the paired order), and the first of them for lane group g.
+template <int NT, bool kPaired>
+__device__ __forceinline__ constexpr int unit_keys(int t0) {
+    return kPaired && t0 + 1 < NT ? 8 : 4;
+}
+template <int NT, bool kPaired>
+__device__ __forceinline__ int unit_key0(int t0, int g) {
+    return unit_keys<NT, kPaired>(t0) == 8 ? 16 * t0 + 8 * g : 16 * t0 + 4 * g;
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -425,6 +448,26 @@ __device__ __forceinline__ char* uniform_ptr(const void* ptr) {
     return reinterpret_cast<char*>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
+// Buffer loads are range-checked per dword of the resource: an [N, N]
+// extent of 16-bit values that ends in the middle of a dword would read the
+// dword holding key N - 1 of row N - 1 as 0.  The bias and mask resources
+// therefore start at the extent's base rounded down to 4 bytes (`lead`, 0
+// or 2, is added to every offset) and span a whole number of dwords: every
+// dword a lane loads is then a 4-aligned word holding at least one byte of
+// the extent, so it lies in a mapped page, and its bytes past the extent
+// (keys >= N) are masked by the -inf of the bias tiles.
+struct AlignedRsrc {
+    __amdgpu_buffer_rsrc_t rs;
+    int lead;  // bytes from the resource base to the extent's first byte
+};
+__device__ __forceinline__ AlignedRsrc aligned_rsrc(const char* base, int64_t bytes) {
+    char* ub = uniform_ptr(base);
+    const int lead = static_cast<int>(reinterpret_cast<uintptr_t>(ub) & 3);
+    const int extent = __builtin_amdgcn_readfirstlane(static_cast<int>((bytes + lead + 3) & ~int64_t(3)));
+    return {__builtin_amdgcn_make_buffer_rsrc(ub - lead, 0, extent, 0x00020000), lead};
+}
+
+
 // 2-byte element types keep V row-major in LDS (like K) and read the
 // V^T MFMA fragments with the gfx950 LDS transpose read: within each group
 // of 16 lanes, lane j receives element j%4 of the 8-byte vectors addressed by
@@ -640,7 +683,7 @@ struct Stage<T, NT, true> {
     // fetches sets the layout.
     //  - One head (h): round r of wave w fills rows 32*(4r + w) .. +31, K in
     //    the kidx tile layout, V as plain 32-byte rows (its transpose reads
-    //    are conflict-free).
+    //    are conflict-free); row u holds key key_of<NT, kPaired>(u).
     //  - kHeadsPerWg heads (h0 ..): token records (kRecStride elements),
     //    load j = wave + 4 * kHeadsPerWg * r of the workgroup's loads fills
     //    chunks 64j .. 64j + 63: chunk c is token c / 13, piece c % 13 (pieces
@@ -648,7 +691,7 @@ struct Stage<T, NT, true> {
     //    V, which lies p.kv_delta elements after K; piece 12 pads the record
     //    and reloads piece 0).  The last load may run past the last record
     //    into the buffer's padding.
-    template <bool kRecs>
+    template <bool kRecs, bool kPaired = false>
     static __device__ __forceinline__ void dma_round(const Params& p, int b, int h, int h0, T* k_dst, T* v_dst,
                                                      int r) {
         static_assert(kDma, "LDS-DMA staging");
@@ -665,11 +708,12 @@ struct Stage<T, NT, true> {
             if (row0 < kRows) {  // wave-uniform
                 const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
                 const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
-                // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15)
-                const int nk = min(row0 + ((lane >> 5) << 4) + (lane & 15), N - 1);
+                // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15);
+                // LDS row u holds key key_of(u)
+                const int nk = min(key_of<NT, kPaired>(row0 + ((lane >> 5) << 4) + (lane & 15)), N - 1);
                 const int hk = ((lane >> 4) & 1) * 8;
                 dma16(kd, kl + row0 * 32, (nk * ks2 + hk) * es);
-                const int nv = min(row0 + (lane >> 1), N - 1);
+                const int nv = min(key_of<NT, kPaired>(row0 + (lane >> 1)), N - 1);
                 dma16(vd, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
             }
         } else {
@@ -712,30 +756,30 @@ struct Stage<T, NT, true> {
 };
 
 // Bias (+ region mask) tiles of one strip, built in registers from the
-// caller's bias tensor: lane (col, g) holds keys 16t + 4g + r of query qi.
-// The head's [N, N] bias is read through a buffer descriptor; keys past N
-// read 0 or the next row and are replaced by -inf (probability exactly 0).
-// Padded query rows get 0 (never stored).  In region mode a key whose
-// shift-region class differs from the query's on an axis that the window
-// type `code` splits gets -100.  kLog2: the tiles are kept in log2 units
-// (multiplied by log2(e)) plus the query's row offset `off`, for the offset
-// softmax of the 2-byte types (attend_offset).  Runs when the window type
-// changes (at most 8 times per workgroup) or the offsets move, never per
-// window otherwise.
+// caller's bias tensor: lane (col, g) holds keys key_of<NT, kPairs>(16t +
+// 4g + r) of query qi.  The head's [N, N] bias is read through a buffer
+// descriptor; keys past N read 0 or the next row and are replaced by -inf
+// (probability exactly 0).  Padded query rows get 0 (never stored).  In
+// region mode a key whose shift-region class differs from the query's on
+// an axis that the window type `code` splits gets -100.  kLog2: the tiles
+// are kept in log2 units (multiplied by log2(e)) plus the query's row offset
+// `off`, for the offset softmax of the 2-byte types (attend_offset).  Runs
+// when the window type changes (at most 8 times per workgroup) or the
+// offsets move, never per window otherwise.
 //
-// A lane's 4 keys of a tile are consecutive in its bias row, so each tile
-// is one load, and all of a wave's loads are issued before any is used (one
-// memory round trip per build).  16-bit rows of an odd row stride start in
-// the middle of a dword and unaligned loads are slow, so those lanes load
-// the three dwords around their keys from a dword-aligned offset and shift
-// the halves into place (shift: 0 or 16 bits).  The last tile of row N-1
-// can reach past the descriptor's extent, where a range check at dword
-// granularity could zero in-range keys: those lanes read that tile again
-// element by element.  (Bias rows never overlap: the host checks that the
-// row stride is at least N.)
-template <int NT, int kMask, bool kLog2, int kBiasDtype>
-__device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_rsrc_t rs, int N, int64_t bsd1,
-                                               int qi, int g, int code, const uint8_t* cls, float off) {
+// A lane's keys of one load unit (a tile, or a pair of tiles in the paired
+// key order) are consecutive in its bias row, so each unit is one load, and
+// all of a wave's loads are issued before any is used (one memory round
+// trip per build).  16-bit rows of an odd row stride start in the middle of
+// a dword and unaligned loads are slow, so those lanes load the dwords
+// around their keys from a dword-aligned offset and shift the halves into
+// place (shift: 0 or 16 bits).  The resource is dword-aligned
+// (aligned_rsrc).  (Bias rows never overlap: the host checks that the row
+// stride is at least N.)
+template <int NT, int kMask, bool kLog2, int kBiasDtype, bool kPaired>
+__device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_rsrc_t rs, int lead, int N,
+                                               int64_t bsd1, int qi, int g, int code, const uint8_t* cls,
+                                               float off) {
     constexpr int kEs = kBiasDtype == CRUMPET_DTYPE_F32 ? 4 : 2;
     // Opaque copies of the lane's position and N: what the build derives from
     // them (per-key validity, offsets) is then computed here, each time,
@@ -744,101 +788,99 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
     asm volatile("" : "+v"(qi), "+v"(g), "+s"(N));
     const bool row = qi < N;
     const int qr = row ? qi : N - 1;
-    const int e0 = static_cast<int>(int64_t(qr) * bsd1 + 4 * g);  // element offset of tile 0's keys
-    constexpr int kTileBytes = 16 * kEs;
-    constexpr int kWords = kEs == 4 ? 4 : 3;
-    const int shift = kEs == 2 ? (e0 & 1) * 16 : 0;
-    const int voff = kEs == 2 ? (e0 & ~1) * 2 : e0 * 4;
+    const int rb = lead + static_cast<int>(int64_t(qr) * bsd1) * kEs;  // byte offset of the row
+    const int shift = (rb & 2) * 8;                                     // 16-bit rows: 0 or 16
+    const int rowb = rb & ~3;                                           // dword-aligned
     uint32_t cq = 0, cmask = 0;
     if constexpr (kMask == kMaskRegion) {
         cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
         cmask = uint32_t(code) * 0x01010101u;
     }
-    // Two halves of the tiles, each: all loads, then the conversions (the
-    // raw words of every tile at once would not fit next to the tiles).
-    constexpr int kHalf = (NT + 1) / 2;
+    // load units: tiles, or pairs of tiles (a lone last tile on its own)
+    constexpr int kUnits = kPaired ? (NT + 1) / 2 : NT;
+    constexpr int kMaxKeys = kPaired && NT > 1 ? 8 : 4;
+    constexpr int kWords = kEs == 4 ? kMaxKeys : kMaxKeys / 2 + 1;
+    // Two halves of the units, each: all loads, then the conversions (the
+    // raw words of every unit at once would not fit next to the tiles).
+    constexpr int kHalf = (kUnits + 1) / 2;
 #pragma unroll
-    for (int t0 = 0; t0 < NT; t0 += kHalf) {
+    for (int u0 = 0; u0 < kUnits; u0 += kHalf) {
         __builtin_amdgcn_sched_barrier(0);
         uint32_t raw[kHalf][kWords];
 #pragma unroll
         for (int u = 0; u < kHalf; ++u) {
-            const int t = t0 + u;
-            if (t >= NT) break;
+            const int un = u0 + u;
+            if (un >= kUnits) break;
+            const int t0 = kPaired ? 2 * un : un;      // first tile of the unit
+            const int nk = unit_keys<NT, kPaired>(t0);  // keys per lane: 4 or 8
+            const int o = rowb + unit_key0<NT, kPaired>(t0, g) * kEs;
             if constexpr (kEs == 4) {
-                const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, voff + kTileBytes * t, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) raw[u][i] = w[i];
+                for (int h = 0; h < nk / 4; ++h) {
+                    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 * h, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) raw[u][4 * h + i < kWords ? 4 * h + i : kWords - 1] = w[i];
+                }
+            } else if (kMaxKeys == 8 && nk == 8) {
+                // (indices clamped: kWords is 5 whenever a unit has 8 keys)
+                const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) raw[u][i < kWords ? i : kWords - 1] = w[i];
+                raw[u][kWords - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 16, 0, 0);
             } else {
-                const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rs, voff + kTileBytes * t, 0, 0);
+                const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rs, o, 0, 0);
 #pragma unroll
                 for (int i = 0; i < 3; ++i) raw[u][i] = w[i];
             }
         }
 #pragma unroll
         for (int u = 0; u < kHalf; ++u) {
-            const int tl = t0 + u;
-            if (kEs == 4 || tl >= NT || !holds_last_key<NT>(tl, qr, g, N)) continue;
-            // the tile holding the last key of the last row (16-bit), element
-            // by element, laid out as the vector load would have returned it
-            {
-                uint32_t kv[4];
+            const int un = u0 + u;
+            if (un >= kUnits) break;
+            const int t0 = kPaired ? 2 * un : un;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    kv[r] = __builtin_amdgcn_raw_buffer_load_b16(rs, voff + shift / 8 + kTileBytes * tl + 2 * r, 0, 0);
-                if (shift != 0) {
-                    raw[u][0] = kv[0] << 16;
-                    raw[u][1] = kv[1] | (kv[2] << 16);
-                    raw[u][2] = kv[3];
+            for (int j = 0; j < unit_keys<NT, kPaired>(t0) / 4; ++j) {
+                const int t = t0 + j;
+                // one tile at a time: scheduled together, the per-key lane
+                // masks of all tiles would not fit the scalar registers
+                __builtin_amdgcn_sched_barrier(0);
+                const int k4 = unit_key0<NT, kPaired>(t0, g) + 4 * j;  // the tile's 4 keys
+                uint32_t split = 0;  // byte r nonzero: key k4 + r is masked by the region rule
+                if constexpr (kMask == kMaskRegion)
+                    split = (*reinterpret_cast<const uint32_t*>(&cls[k4]) ^ cq) & cmask;
+                float v4[4];
+                if constexpr (kEs == 4) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v4[r] = __uint_as_float(raw[u][4 * j + r]);
                 } else {
-                    raw[u][0] = kv[0] | (kv[1] << 16);
-                    raw[u][1] = kv[2] | (kv[3] << 16);
-                    raw[u][2] = 0u;
+                    const uint32_t hw[2] = {__builtin_amdgcn_alignbit(raw[u][2 * j + 1], raw[u][2 * j], shift),
+                                            __builtin_amdgcn_alignbit(raw[u][2 * j + 2], raw[u][2 * j + 1], shift)};
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const uint32_t bits = (r & 1) ? hw[r >> 1] >> 16 : hw[r >> 1] & 0xffffu;
+                        if constexpr (kBiasDtype == CRUMPET_DTYPE_BF16)
+                            v4[r] = __uint_as_float(bits << 16);
+                        else
+                            v4[r] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+                    }
                 }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kHalf; ++u) {
-            const int t = t0 + u;
-            if (t >= NT) break;
-            // one tile at a time: scheduled together, the per-key lane masks
-            // of all tiles would not fit the scalar registers
-            __builtin_amdgcn_sched_barrier(0);
-            uint32_t split = 0;  // byte r nonzero: key 16t+4g+r is masked by the region rule
-            if constexpr (kMask == kMaskRegion)
-                split = (*reinterpret_cast<const uint32_t*>(&cls[16 * t + 4 * g]) ^ cq) & cmask;
-            float v4[4];
-            if constexpr (kEs == 4) {
-#pragma unroll
-                for (int r = 0; r < 4; ++r) v4[r] = __uint_as_float(raw[u][r]);
-            } else {
-                const uint32_t hw[2] = {__builtin_amdgcn_alignbit(raw[u][1], raw[u][0], shift),
-                                        __builtin_amdgcn_alignbit(raw[u][2], raw[u][1], shift)};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const uint32_t bits = (r & 1) ? hw[r >> 1] >> 16 : hw[r >> 1] & 0xffffu;
-                    if constexpr (kBiasDtype == CRUMPET_DTYPE_BF16)
-                        v4[r] = __uint_as_float(bits << 16);
-                    else
-                        v4[r] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+                    float val = v4[r];
+                    if constexpr (kMask == kMaskRegion) {
+                        if ((split >> (8 * r)) & 0xffu) val += -100.0f;
+                    }
+                    if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
+                    val = row ? val : 0.0f;
+                    bs[t][r] = (k4 + r) < N ? val : -INFINITY;
                 }
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float val = v4[r];
-                if constexpr (kMask == kMaskRegion) {
-                    if ((split >> (8 * r)) & 0xffu) val += -100.0f;
-                }
-                if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
-                val = row ? val : 0.0f;
-                bs[t][r] = (16 * t + 4 * g + r) < N ? val : -INFINITY;
             }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NT, int kMask, bool kLog2>
+template <int NT, int kMask, bool kLog2, bool kPaired>
 __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, int h, int qi, int g,
                                             int code, const uint8_t* cls, float off) {
     // Re-read the kernel arguments (Params is the kernel's only argument, at
@@ -856,17 +898,18 @@ __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, 
     const int es = bias_dtype == CRUMPET_DTYPE_F32 ? 4 : 2;
     // base and extent are workgroup-uniform; readfirstlane keeps the
     // descriptor in SGPRs (a VGPR descriptor costs a waterfall loop per load)
-    char* hb = uniform_ptr(static_cast<const char*>(bias_ptr) + int64_t(h) * bsd0 * es);
-    const int extent =
-        __builtin_amdgcn_readfirstlane(static_cast<int>((int64_t(N - 1) * bsd1 + N) * es));
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(hb, 0, extent, 0x00020000);
+    const AlignedRsrc ar = aligned_rsrc(static_cast<const char*>(bias_ptr) + int64_t(h) * bsd0 * es,
+                                        (int64_t(N - 1) * bsd1 + N) * es);
     // uniform: one dtype branch per build, none per tile or element
     if (bias_dtype == CRUMPET_DTYPE_F32)
-        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F32>(bs, rs, N, bsd1, qi, g, code, cls, off);
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F32, kPaired>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls,
+                                                                       off);
     else if (bias_dtype == CRUMPET_DTYPE_BF16)
-        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_BF16>(bs, rs, N, bsd1, qi, g, code, cls, off);
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_BF16, kPaired>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls,
+                                                                       off);
     else
-        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F16>(bs, rs, N, bsd1, qi, g, code, cls, off);
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F16, kPaired>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls,
+                                                                       off);
 }
 
 
@@ -916,7 +959,7 @@ constexpr float kRowSumLimit = 32768.0f;  // row sums (hence every P) stay below
 // attend_offset spreads them over its tile pairs, so that a workgroup's
 // loads reach the memory pipeline a few at a time while it computes instead
 // of all at the window start (where every wave would stall on issue).
-template <typename T, typename St, bool kRecs>
+template <typename T, typename St, bool kRecs, bool kPaired>
 struct DmaIssuer {
     static constexpr int kRounds = St::template dma_rounds<kRecs>();
     const Params* p;
@@ -925,7 +968,7 @@ struct DmaIssuer {
     T* v_dst;
     bool on;  // a next window exists (wave-uniform)
     __device__ __forceinline__ void operator()(int r) const {
-        if (on) St::template dma_round<kRecs>(*p, b, h, h0, k_dst, v_dst, r);
+        if (on) St::template dma_round<kRecs, kPaired>(*p, b, h, h0, k_dst, v_dst, r);
     }
 };
 struct NoIssue {
@@ -933,7 +976,7 @@ struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
 
-template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, typename Issue>
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, bool kPaired, typename Issue>
 __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
                                               const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
                                               int h, int wave, int qi, int col, int g, float& off,
@@ -964,77 +1007,75 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     int mvoff = 0;
     if constexpr (kUseMask) {
         const int qr = qi < N ? qi : N - 1;
-        char* mb = uniform_ptr(static_cast<const char*>(p.mask) +
-                               int64_t(b % p.mask_batch) * p.ms[0] * kMaskBytes);
-        const int extent =
-            __builtin_amdgcn_readfirstlane(static_cast<int>(((N - 1) * p.ms[1] + N) * kMaskBytes));
-        mrsrc = __builtin_amdgcn_make_buffer_rsrc(mb, 0, extent, 0x00020000);
-        mvoff = static_cast<int>((qr * p.ms[1] + 4 * g) * kMaskBytes);
+        const AlignedRsrc ar =
+            aligned_rsrc(static_cast<const char*>(p.mask) + int64_t(b % p.mask_batch) * p.ms[0] * kMaskBytes,
+                         int64_t((N - 1) * p.ms[1] + N) * kMaskBytes);
+        mrsrc = ar.rs;
+        mvoff = ar.lead + static_cast<int>(qr * p.ms[1] * kMaskBytes);
     }
+    // Mask values by load unit (a tile, or in the paired key order a pair of
+    // tiles: key_of), each lane's keys of a unit consecutive in its row.
     // 2-byte masks: a row of an odd row stride starts in the middle of a
-    // dword, and unaligned 8-byte loads are slow.  Each lane therefore loads
-    // the three dwords around its 4 keys from a dword-aligned offset and
-    // shifts its halves into place when it uses them (mshift: 0 or 16 bits).
-    // The words held per tile: 3 (2-byte) or 4 (fp32).
+    // dword, and unaligned loads are slow.  Each lane therefore loads the
+    // dwords around its keys from a dword-aligned offset (mvoff is the row's,
+    // in a dword-aligned resource: aligned_rsrc) and shifts its halves into
+    // place when it uses them (mshift: 0 or 16 bits).  Words per unit: 2-byte
+    // 3 (4 keys) or 5 (8 keys), fp32 4 or 8.
     int mshift = 0;
     if constexpr (kUseMask && kMaskBytes == 2) {
         mshift = (mvoff & 2) * 8;
         mvoff &= ~3;
     }
-    constexpr int kMWords = kMaskBytes == 2 ? 3 : 4;
+    constexpr int kMaxKeys = kPaired && NT > 1 ? 8 : 4;
+    constexpr int kMWords = kMaskBytes == 2 ? kMaxKeys / 2 + 1 : kMaxKeys;
     typedef uint32_t MaskWords[kMWords];
+    // the first tile of the load unit holding tile t (compile-time)
+    auto unit_of = [](int t) { return kPaired && (t & 1) ? t - 1 : t; };
+    // the words of the unit starting at tile t
     auto fetch = [&](int t, MaskWords& w) {
         if constexpr (kUseMask) {
-            const int o = mvoff + 16 * t * kMaskBytes;
+            const int nk = unit_keys<NT, kPaired>(t);
+            const int k0 = unit_key0<NT, kPaired>(t, g);
+            const int o = mvoff + k0 * kMaskBytes;
             if constexpr (kMaskBytes == 2) {
-                const u32x3 v3 = __builtin_amdgcn_raw_buffer_load_b96(mrsrc, o, 0, 0);
-                w[0] = v3[0];
-                w[1] = v3[1];
-                w[2] = v3[2];
-            } else {
-                const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o, 0, 0);
+                if (kMaxKeys == 8 && nk == 8) {
+                    // (indices clamped: kMWords is 5 whenever a unit has 8 keys)
+                    const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o, 0, 0);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) w[r] = v4[r];
-            }
-            if (kMaskBytes == 2 && holds_last_key<NT>(t, qi, g, N)) {
-                // 16-bit keys of the last row holding key N - 1: element by
-                // element, laid out as the three dwords would hold them
-                if constexpr (kMaskBytes == 2) {
-                    uint32_t kv[4];
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        kv[r] = __builtin_amdgcn_raw_buffer_load_b16(mrsrc, o + mshift / 8 + 2 * r, 0, 0);
-                    if (mshift != 0) {
-                        w[0] = kv[0] << 16;
-                        w[1] = kv[1] | (kv[2] << 16);
-                        w[2] = kv[3];
-                    } else {
-                        w[0] = kv[0] | (kv[1] << 16);
-                        w[1] = kv[2] | (kv[3] << 16);
-                        w[2] = 0u;
-                    }
+                    for (int r = 0; r < 4; ++r) w[r < kMWords ? r : kMWords - 1] = v4[r];
+                    w[kMWords - 1] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, o + 16, 0, 0);
                 } else {
+                    const u32x3 v3 = __builtin_amdgcn_raw_buffer_load_b96(mrsrc, o, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) w[r] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, o + 4 * r, 0, 0);
+                    for (int r = 0; r < 3; ++r) w[r] = v3[r];
+                }
+            } else {
+#pragma unroll
+                for (int hh = 0; hh < nk / 4; ++hh) {
+                    const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o + 16 * hh, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) w[4 * hh + r < kMWords ? 4 * hh + r : kMWords - 1] = v4[r];
                 }
             }
         }
     };
     // accumulator input of tile t: bias (+ region mask) tile with the row
-    // offset, plus the mask tensor's values in log2 units
+    // offset, plus the mask tensor's values in log2 units (w: the words of
+    // the unit holding tile t)
     auto cinit = [&](int t, const MaskWords& w) -> f32x4 {
         f32x4 c = bs[t];
         if constexpr (kUseMask) {
-            uint32_t hw[2] = {0u, 0u};  // 2-byte masks: the 4 keys' halves in place
+            const int j = t - unit_of(t);  // the tile's place in its unit
+            uint32_t hw[2] = {0u, 0u};     // 2-byte masks: the 4 keys' halves in place
             if constexpr (kMaskBytes == 2) {
-                hw[0] = __builtin_amdgcn_alignbit(w[1], w[0], mshift);
-                hw[1] = __builtin_amdgcn_alignbit(w[2], w[1], mshift);
+                hw[0] = __builtin_amdgcn_alignbit(w[2 * j + 1], w[2 * j], mshift);
+                hw[1] = __builtin_amdgcn_alignbit(w[2 * j + 2], w[2 * j + 1], mshift);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float mv;
                 if constexpr (kMask == kMaskF32)
-                    mv = __uint_as_float(w[r]);
+                    mv = __uint_as_float(w[4 * j + r]);
                 else if constexpr (kMask == kMaskF16)
                     mv = static_cast<float>(
                         __builtin_bit_cast(_Float16, static_cast<uint16_t>(r & 1 ? hw[r >> 1] >> 16 : hw[r >> 1])));
@@ -1098,10 +1139,12 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         for (int t = 0; t < NT && t < 2 * kKAhead; ++t) kf[t] = kfrag(t);
         if constexpr (kUseMask) {
 #pragma unroll
-            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t) fetch(t, mw[t]);
+            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t)
+                if (unit_of(t) == t) fetch(t, mw[t]);
         }
 #pragma unroll
-        for (int t = 0; t < NT && t < 2; ++t) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
+        for (int t = 0; t < NT && t < 2; ++t)
+            S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? unit_of(t) : 0]));
 #pragma unroll
         for (int pr = 0; pr < kPairs; ++pr) {
             __builtin_amdgcn_sched_barrier(0);
@@ -1120,7 +1163,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             if constexpr (kUseMask) {
 #pragma unroll
                 for (int t = t0 + 2 * kMaskAhead; t < t0 + 2 * kMaskAhead + 2; ++t)
-                    if (t < NT) fetch(t, mw[t]);
+                    if (t < NT && unit_of(t) == t) fetch(t, mw[t]);
             }
             X8 pb;
             if constexpr (kKAhead == 1) {
@@ -1129,7 +1172,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             }
 #pragma unroll
             for (int t = t0 + 2; t < t0 + 4; ++t)
-                if (t < NT) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
+                if (t < NT) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? unit_of(t) : 0]));
             if constexpr (kKAhead != 1) pb = probs(S[t0], S[has1 ? t0 + 1 : t0], has1);
             accumulate(pb, v0, v1, has1, o, lacc);
             asm volatile("" : "+v"(o));  // as in the exact pass below
@@ -1151,11 +1194,11 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         asm volatile("" : "+v"(ka), "+v"(mva));
         mvoff = mva;
         float m0 = -INFINITY, m1 = -INFINITY;
+        MaskWords w;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             __builtin_amdgcn_sched_barrier(0);
-            MaskWords w;
-            fetch(t, w);
+            if (unit_of(t) == t) fetch(t, w);
             const f32x4 sc = Frag<T>::mma32(lds_load<X8>(ka + t * kKTile * sizeof(T)), qf, cinit(t, w));
             m0 = fmaxf(fmaxf(m0, sc[0]), sc[1]);
             m1 = fmaxf(fmaxf(m1, sc[2]), sc[3]);
@@ -1178,11 +1221,12 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             const bool has1 = t0 + 1 < NT;
             MaskWords w0, w1;
             fetch(t0, w0);
-            if (has1) fetch(t0 + 1, w1);
+            if (has1 && unit_of(t0 + 1) != t0) fetch(t0 + 1, w1);
+            const MaskWords& w1u = unit_of(t0 + 1) == t0 ? w0 : w1;
             const f32x4 s0 = Frag<T>::mma32(lds_load<X8>(kb + t0 * kKTile * sizeof(T)), qf, cinit(t0, w0) - m);
             f32x4 s1 = s0;
             if (has1)
-                s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), qf, cinit(t0 + 1, w1) - m);
+                s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), qf, cinit(t0 + 1, w1u) - m);
             const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
             const X4 v1 = has1 ? lds_read_tr<T>(vrow + kVTile * (t0 + 1)) : v0;
             accumulate(probs(s0, s1, has1), v0, v1, has1, o, lacc);
@@ -1273,7 +1317,7 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
             }
             // the 16-bit keys of the last row holding key N - 1 are read again
             // element by element
-            if (kMaskBytes == 2 && holds_last_key<NT>(t, qi, g, N)) {
+            if (kMaskBytes == 2 && t >= first_last_tile(NT) && holds_last_key(16 * t + 4 * g, 4, qi, N)) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     if constexpr (kMaskBytes == 2) {
@@ -1416,6 +1460,8 @@ swin_attention_d16_kernel(const Params p) {
     constexpr int kQBufs = HPW > 1 ? 1 : 2;
     static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
     constexpr bool kRecs = HPW > 1;  // token-record K/V layout shared by the head slots
+    // paired key order (key_of) on the LDS-DMA path with a mask tensor
+    constexpr bool kPaired = kVec && v_row_major<T>() && mask_tensor(kMask);
     // (kRecs: K and V in one record array, k_lds; the last load's spill
     // lands in its padding)
     constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * 16;
@@ -1503,7 +1549,7 @@ swin_attention_d16_kernel(const Params p) {
             st.load_q(p, bw, h, q0);
 #pragma unroll
             for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r)
-                St::template dma_round<kRecs>(p, bw, h, h0, k_lds[sb], vt_lds[sb], r);
+                St::template dma_round<kRecs, kPaired>(p, bw, h, h0, k_lds[sb], vt_lds[sb], r);
         } else {
             st.load(p, bw, h, q0, k_lds[sb], vt_lds[sb]);
         }
@@ -1524,7 +1570,7 @@ swin_attention_d16_kernel(const Params p) {
         // waiting for the bias loads after that request would wait for the
         // rows as well.
         if (active && (code != code_cur || rebuild)) {  // code is workgroup-uniform
-            build_tiles<NT, kMask, sizeof(T) == 2>(bs, p, h, qi, g, code, cls_lds, off);
+            build_tiles<NT, kMask, sizeof(T) == 2, kPaired>(bs, p, h, qi, g, code, cls_lds, off);
             code_cur = code;
             rebuild = false;
         }
@@ -1544,7 +1590,8 @@ swin_attention_d16_kernel(const Params p) {
         }
         const auto issue = [&]() {
             if constexpr (kSpread)
-                return DmaIssuer<T, St, kRecs>{&p, b_next, h, h0, k_lds[buf ^ 1], vt_lds[buf ^ 1], i + 1 < i1};
+                return DmaIssuer<T, St, kRecs, kPaired>{&p, b_next, h, h0, k_lds[buf ^ 1], vt_lds[buf ^ 1],
+                                                         i + 1 < i1};
             else
                 return NoIssue{};
         }();
@@ -1559,10 +1606,10 @@ swin_attention_d16_kernel(const Params p) {
             if constexpr (kTensor) use_mask = flag;
             if constexpr (sizeof(T) == 2) {
                 if (use_mask)
-                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, Issuer>(
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, kPaired, Issuer>(
                         p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
                 else
-                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, Issuer>(
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, kPaired, Issuer>(
                         p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
             } else {
                 if (use_mask)
