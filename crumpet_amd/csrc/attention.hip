@@ -210,9 +210,9 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.strips = static_cast<int32_t>((N + 15) / 16);
     p.groups = (p.strips + attn::kWaves - 1) / attn::kWaves;
     // several heads per workgroup: 2-byte LDS-DMA path, large windows, no
-    // mask tensor, H a multiple, heads adjacent in the K and V rows and V at
-    // a fixed distance after K (same strides), addressed from K's base with
-    // 32-bit byte offsets
+    // mask tensor or a 16-bit one without boundary flags, H a multiple, heads
+    // adjacent in the K and V rows and V at a fixed distance after K (same
+    // strides), addressed from K's base with 32-bit byte offsets
     const int64_t kv_bytes = static_cast<const char*>(v) - static_cast<const char*>(k);
     const bool records = k_strides[1] == 16 && v_strides[1] == 16 && k_strides[0] == v_strides[0] &&
                          k_strides[2] == v_strides[2] && kv_bytes >= 0 && kv_bytes % esize == 0 &&
@@ -220,7 +220,8 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                          ((N - 1) * k_strides[2] + kv_bytes / esize + 16 * attn::kHeadsPerWg) * esize <
                              (int64_t(1) << 31);
     p.hpw = (dtype != CRUMPET_DTYPE_F32 && p.vec_io && attn::multi_head_tiles(NT) &&
-             !attn::mask_tensor(kmask) && Hh % attn::kHeadsPerWg == 0 && records)
+             (!attn::mask_tensor(kmask) || (boundary == nullptr && kmask != attn::kMaskF32)) &&
+             Hh % attn::kHeadsPerWg == 0 && records)
                 ? attn::kHeadsPerWg
                 : 1;
     p.kv_delta = p.hpw > 1 ? static_cast<int32_t>(kv_bytes / esize) : 0;

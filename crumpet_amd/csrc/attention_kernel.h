@@ -86,13 +86,15 @@ namespace attn {
 
 constexpr int kWaves = 4;  // waves (strips) per workgroup
 constexpr int kThreads = 64 * kWaves;  // threads per head slot of a workgroup
-// Heads per workgroup on the LDS-DMA path without a mask tensor, when H is
-// a multiple of it and the heads of a token are adjacent (head stride 16,
-// as in the usual [token][3][H][Dh] qkv layout): the workgroup runs the
-// kWaves strips of each of its heads and stages their K and V together as
-// token records (below), so that its loads read contiguous bytes.  With a
-// mask tensor the heads' waves would all load the same mask rows at once;
-// those launches keep one head per workgroup.
+// Heads per workgroup on the LDS-DMA path when H is a multiple of it and
+// the heads of a token are adjacent (head stride 16, as in the usual
+// [token][3][H][Dh] qkv layout): the workgroup runs the kWaves strips of
+// each of its heads and stages their K and V together as token records
+// (below), so that its loads read contiguous bytes.  With a mask tensor and
+// boundary flags, one head per workgroup is faster (config 3: 186 against
+// 237 us; with every window masked 270 against 238 us): those launches
+// keep it, and so do fp32 masks (their loop needs more registers than 12
+// waves per CU leave).
 constexpr int kHeadsPerWg = 3;
 // Tile counts with a kHeadsPerWg variant: the large windows, where K/V
 // staging dominates and 3 heads' double-buffered K/V still fit one CU's LDS.
@@ -728,10 +730,10 @@ struct Stage<T, NT, true> {
                 const u32x4 d = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N,
                                               kvd + 16 * kHeadsPerWg);
                 const int c = 64 * j + lane;
-                const int n = c / 13;
+                const int n = c / 13;  // record n holds token key_of(n)
                 const int piece = c - 13 * n;
                 const int part = piece < 6 ? 8 * piece : (piece < 12 ? kvd + 8 * (piece - 6) : 0);
-                dma16(d, kl + j * 1024, (min(n, N - 1) * ks2 + part) * es);
+                dma16(d, kl + j * 1024, (min(key_of<NT, kPaired>(n), N - 1) * ks2 + part) * es);
             }
         }
     }
@@ -1632,7 +1634,7 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
 #define CRUMPET_ATTN_MASK(NTV, MK)                                                                    \
     do {                                                                                              \
         if (p.vec_io) {                                                                               \
-            if constexpr (v_row_major<T>() && multi_head_tiles(NTV) && !mask_tensor(MK)) {            \
+            if constexpr (v_row_major<T>() && multi_head_tiles(NTV) && MK != kMaskF32) {              \
                 if (p.hpw == kHeadsPerWg) {                                                           \
                     hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true, kHeadsPerWg>), grid, \
                                        block, 0, s, p);                                               \

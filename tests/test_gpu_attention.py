@@ -340,14 +340,17 @@ def _interleaved(B, N, H, dtype, seed):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("H", [3, 6])
 @pytest.mark.parametrize("ws", [(6, 6, 6), (7, 7, 7)])
-@pytest.mark.parametrize("shifted", [True, False], ids=["region", "nomask"])
-def test_head_records_interleaved_qkv(oracle, dev, dtype, H, ws, shifted):
+@pytest.mark.parametrize("mode", ["region", "nomask", "tensor"])
+def test_head_records_interleaved_qkv(oracle, dev, dtype, H, ws, mode):
     """Interleaved qkv with H a multiple of 3 runs three heads per workgroup
     with K/V staged as token records (N = 216 and 343: both tile counts that
-    have that variant); every window against the oracle, and against the
-    same data in separate contiguous tensors (one head per workgroup)."""
+    have that variant), also with a mask tensor and no boundary flags (every
+    window masked, paired key order); every window against the oracle, and
+    against the same data in separate contiguous tensors (one head per
+    workgroup)."""
     from crumpet_amd.fused_attention import fused_swin_attention_shifted
 
+    shifted = mode != "nomask"
     vol = tuple(2 * w for w in ws)
     ss = tuple(w // 2 for w in ws) if shifted else (0, 0, 0)
     N = ws[0] * ws[1] * ws[2]
@@ -361,16 +364,17 @@ def test_head_records_interleaved_qkv(oracle, dev, dtype, H, ws, shifted):
     td = qkv.to(dev).reshape(B, N, 3, H, 16).permute(2, 0, 3, 1, 4)
     out_bnc = torch.empty((B, N, H * 16), dtype=dtype, device=dev)
     out = out_bnc.view(B, N, H, 16).permute(0, 2, 1, 3)
-    if shifted:
+    mask_t = None if m is None else torch.from_numpy(np.ascontiguousarray(m[np.arange(B) % 8])).to(dtype).to(dev)
+    if mode == "region":
         fused_swin_attention_shifted(td[0], td[1], td[2], bias.to(dev), vol, ws, ss, scale=0.25, out=out)
     else:
-        fused_swin_attention(td[0], td[1], td[2], bias.to(dev), None, scale=0.25, out=out)
-    _compare(out, ref, dtype, f"records H={H} N={N} {'region' if shifted else 'nomask'}")
+        fused_swin_attention(td[0], td[1], td[2], bias.to(dev), mask_t, scale=0.25, out=out)
+    _compare(out, ref, dtype, f"records H={H} N={N} {mode}")
     sep = [x.contiguous() for x in td]
-    if shifted:
+    if mode == "region":
         other = fused_swin_attention_shifted(sep[0], sep[1], sep[2], bias.to(dev), vol, ws, ss, scale=0.25)
     else:
-        other = fused_swin_attention(sep[0], sep[1], sep[2], bias.to(dev), None, scale=0.25)
+        other = fused_swin_attention(sep[0], sep[1], sep[2], bias.to(dev), mask_t, scale=0.25)
     diff = (out.float() - other.float()).abs().max().item()
     assert diff <= TOL[dtype], diff
 
