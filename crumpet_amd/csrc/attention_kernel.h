@@ -10,23 +10,31 @@
 //
 // Work decomposition (bias-stationary, persistent)
 //   The relative-position bias is the same for every window, so it is kept in
-//   registers instead of being re-read per window: a workgroup of 4 waves
-//   owns one head h and a group of 4 consecutive 16-query strips, and walks a
-//   range of windows (contiguous; every ranges-th window with a mask tensor,
-//   whose boundary windows cost more and come in runs).  Each wave builds the fp32 bias tiles of its
-//   strip (NT tiles of 16 keys x 16 queries, 4 values per lane each) once,
-//   straight from the caller's bias tensor (any float dtype and strides),
-//   and uses them as the accumulator input of every window's S^T = K Q^T
-//   MFMAs, so the bias add costs neither memory traffic nor VALU work.
+//   registers instead of being re-read per window: a workgroup owns one head
+//   (4 waves) or kHeadsPerWg heads (12 waves) and a group of 4 consecutive
+//   16-query strips of each, and walks a range of windows (contiguous; every
+//   ranges-th window with a mask tensor and boundary flags, whose flagged
+//   windows cost more and come in runs).  Each wave builds the fp32 bias
+//   tiles of its strip (NT tiles of 16 keys x 16 queries, 4 values per lane
+//   each) once, straight from the caller's bias tensor (any float dtype and
+//   strides), and uses them as the accumulator input of every window's
+//   S^T = K Q^T MFMAs, so the bias add costs neither memory traffic nor VALU
+//   work.
 //
-//   Q (the group's 64 rows, pre-scaled and rounded), K and V of a window
-//   live in LDS, double-buffered, one barrier per window.  While the waves
-//   compute window i, window i+1 is fetched into the other buffer: for 2-byte
-//   types with unit d stride, K and V rows go straight from memory to LDS
-//   (buffer loads with the lds flag) and only Q passes through registers;
-//   otherwise each thread holds its share in registers and stores it after
-//   the compute (fp32 keeps V transposed; 2-byte types keep V row-major and
-//   read V^T with the LDS transpose read).
+//   Q (the group's 64 rows per head, pre-scaled and rounded), K and V of a
+//   window live in LDS, K and V double-buffered, one barrier per window.
+//   While the waves compute window i, window i+1 is fetched into the other
+//   buffer: for 2-byte types with unit d stride, K and V rows go straight
+//   from memory to LDS (buffer loads with the lds flag, a few per wave from
+//   inside the tile-pair loop) and only Q passes through registers; with
+//   several heads per workgroup they arrive as token records (all heads' K
+//   rows, then V rows, as they lie in memory), because a vector load moves
+//   whole 128-byte lines.  Otherwise each thread holds its share in
+//   registers and stores it after the compute (fp32 keeps V transposed;
+//   2-byte types keep V row-major and read V^T with the LDS transpose read).
+//   With a mask tensor the 2-byte DMA kernels use the paired key order
+//   (key_of), in which a lane's mask and bias values of two tiles are one
+//   load.
 //
 //   In region mode the windows are visited grouped by type (which axes the
 //   window is last on; at most 8 types).  The shifted-window mask of a window
