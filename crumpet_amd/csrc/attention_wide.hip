@@ -183,6 +183,9 @@ swin_attention_wide_kernel(const Params p, int32_t mask_dtype, uint32_t qblocks,
     __shared__ __attribute__((aligned(16))) T k_lds[2][kKC * kKStride];
     __shared__ __attribute__((aligned(16))) T vt_lds[2][D * kVStride];
     __shared__ uint8_t cls_lds[kMode == 2 ? kWideMaxRegionN : 4];
+    // (fp32 at head dim 128 takes about 70 KB: more than the 64 KB of earlier CDNA parts)
+    static_assert(sizeof(k_lds) + sizeof(vt_lds) + sizeof(cls_lds) <= 160 * 1024,
+                  "LDS footprint exceeds the 160 KB of a gfx950 CU");
 
     uint32_t chunk;
     if (!xcd_chunk(blockIdx.x, launched, chunks, chunk)) return;

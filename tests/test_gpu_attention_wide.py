@@ -129,13 +129,16 @@ def test_non_unit_d_stride_and_odd_offsets(oracle, dev, Dh):
     _compare(out, ref, dtype, f"non-unit d stride Dh={Dh}")
 
 
-@pytest.mark.parametrize("Dh", [16, 32])
+@pytest.mark.parametrize("Dh", [16, 32, 64, 128])
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_shifted_regions_general_kernel(oracle, dev, Dh, dtype):
-    """Region mode of the general kernel: head dim 32 at window 7 (N = 343),
-    and head dim 16 at window 9 (N = 729 > 512), against the
-    compute_attn_mask_3d mask tiled over the outer batch."""
-    vol, ws, ss = ((14, 14, 14), (7, 7, 7), (3, 3, 3)) if Dh == 32 else ((18, 18, 9), (9, 9, 9), (4, 4, 0))
+    """Region mode of the general kernel: head dims 32, 64 and 128 at window
+    7 (N = 343), and head dim 16 at window 9 (N = 729 > 512), against the
+    compute_attn_mask_3d mask tiled over the outer batch.  Head dims 64 and
+    128 use the model's scale Dh^-0.5: at 0.25 their scores spread so far
+    that bf16's rounding of P alone reaches the bf16 tolerance (fp32 runs of
+    the same case agree to 6e-6)."""
+    vol, ws, ss = ((14, 14, 14), (7, 7, 7), (3, 3, 3)) if Dh != 16 else ((18, 18, 9), (9, 9, 9), (4, 4, 0))
     nW = (vol[0] // ws[0]) * (vol[1] // ws[1]) * (vol[2] // ws[2])
     N = ws[0] * ws[1] * ws[2]
     B, H = nW * 2, 2
@@ -143,8 +146,9 @@ def test_shifted_regions_general_kernel(oracle, dev, Dh, dtype):
     rows = (2 * ws[0] - 1) * (2 * ws[1] - 1) * (2 * ws[2] - 1)
     bias = bias_from_table(trunc_normal_table(rows, H, 3401 + N), ws).to(dtype)
     m = oracle.attn_mask(*vol, ws, ss, "float32")
-    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m, None, scale=0.25)
-    out = fused_swin_attention_shifted(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), vol, ws, ss, scale=0.25)
+    scale = 0.25 if Dh <= 32 else Dh ** -0.5
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m, None, scale=scale)
+    out = fused_swin_attention_shifted(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), vol, ws, ss, scale=scale)
     _compare(out, ref, dtype, f"region Dh={Dh} N={N} {dtype}")
 
 
@@ -179,10 +183,12 @@ def patched():
 
 
 @pytest.mark.parametrize("fused_block", ["1", "0"], ids=["unfused-block", "fused-block"])
-def test_patched_basic_layer_head_dim_32(patched, dev, monkeypatch, fused_block):
-    """Feature size 96 (head dim 32): the patched BasicLayer (shifted and
-    unshifted blocks) matches its own eager fp32 forward, through the fused
-    block kernels and through partition / attention / unpartition."""
+@pytest.mark.parametrize("dim", [96, 192], ids=["hd32", "hd64"])
+def test_patched_basic_layer_head_dim_32(patched, dev, monkeypatch, fused_block, dim):
+    """Feature size 96 or 192 with 3 heads (head dim 32 or 64): the patched
+    BasicLayer (shifted and unshifted blocks) matches its own eager fp32
+    forward, through the fused block kernels and through partition /
+    attention / unpartition, both on the general kernel."""
     from crumpet_amd import fused_block as fb
     from crumpet_amd import monai_patch
 
@@ -198,14 +204,37 @@ def test_patched_basic_layer_head_dim_32(patched, dev, monkeypatch, fused_block)
 
             monkeypatch.setattr(mod, name, spy)
     torch.manual_seed(3600)
-    layer = sw.BasicLayer(dim=96, depth=2, num_heads=3, window_size=(7, 7, 7), drop_path=0.0, qkv_bias=True,
+    layer = sw.BasicLayer(dim=dim, depth=2, num_heads=3, window_size=(7, 7, 7), drop_path=0.0, qkv_bias=True,
                           downsample=None).to(dev).eval()
-    x = torch.randn((2, 96, 12, 12, 12), generator=torch.Generator().manual_seed(3601)).to(dev)
+    x = torch.randn((2, dim, 12, 12, 12), generator=torch.Generator().manual_seed(3601)).to(dev)
     with torch.no_grad():
         want = layer(x)
         assert crumpet_amd.patch_monai_swin_unetr()
         got = layer(x)
     err = (got - want).abs().max().item()
-    print(f"head dim 32 basic layer: max-abs {err:.2e}, kernel calls {calls}", flush=True)
+    print(f"head dim {dim // 3} basic layer: max-abs {err:.2e}, kernel calls {calls}", flush=True)
     assert calls == ["fused_swin_attention_windows", "fused_swin_attention_shifted"]
     assert err < 1e-4
+
+
+def test_tuned_and_general_kernels_agree_at_512(oracle, dev):
+    """The same N = 512 problem through both kernels: the tuned one at N = 512
+    and the general one at N = 513 with a -inf bias on key 512 (so its first
+    512 rows solve the same problem).  The tuned kernel sums the rounded P for
+    the row sums, the general one the fp32 P; both agree with the fp32 oracle
+    and with each other within the fp16 tolerance."""
+    dtype, B, H, N, Dh = torch.float16, 2, 2, 512, 16
+    q, k, v = _inputs(B, H, N + 1, Dh, dtype, 3700)
+    bias = seeded((H, N + 1, N + 1), torch.float32, 3701) * 0.1
+    bias[:, :, N] = float("-inf")
+    ref = oracle.attention(_f32(q[:, :, :N]), _f32(k[:, :, :N]), _f32(v[:, :, :N]), _f32(bias[:, :N, :N]),
+                           None, None, scale=0.25)
+    qd, kd, vd, bd = (t.to(dev) for t in (q, k, v, bias))
+    tuned = fused_swin_attention(qd[:, :, :N].contiguous(), kd[:, :, :N].contiguous(), vd[:, :, :N].contiguous(),
+                                 bd[:, :N, :N].contiguous(), None, scale=0.25)
+    general = fused_swin_attention(qd, kd, vd, bd, None, scale=0.25)[:, :, :N]
+    _compare(tuned, ref, dtype, "tuned N=512")
+    _compare(general, ref, dtype, "general N=513, key 512 masked")
+    diff = (tuned.float() - general.float()).abs().max().item()
+    print(f"tuned vs general max-abs {diff:.2e}", flush=True)
+    assert diff <= TOL[dtype], diff
