@@ -419,7 +419,20 @@ struct WindowIter {
     __device__ __forceinline__ int window(const Params& p, int& type_code) const {
         if constexpr (kMask != kMaskRegion) {
             type_code = 0;
-            return base + i * stride;
+            const int L = base + i * stride;
+            if constexpr (kMask != kNoMask) {
+                // mask-major order: the B / M windows that read mask m
+                // (m, m + M, ...) are consecutive logical indices, hence
+                // taken by consecutive ranges (consecutive workgroups, on one
+                // XCD) at the same step, and share the mask rows in its L2
+                const int M = p.mask_batch;
+                if (M > 1 && M < p.B) {
+                    const int copies = p.B / M;
+                    const int m = L / copies;
+                    return (L - m * copies) * M + m;
+                }
+            }
+            return L;
         } else {
             const int wd = (code & 4) ? p.nWd - 1 : jd;
             const int wh = (code & 2) ? p.nWh - 1 : jh;
