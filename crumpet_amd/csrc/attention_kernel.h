@@ -671,7 +671,7 @@ struct Stage<T, NT, true> {
         rq = ld(qr, (nq * qs2 + d0) * es);
         if constexpr (kDma) {
 #pragma unroll
-            for (int r = 0; r < kRounds; ++r) dma_round<false>(p, b, h, h, k_dst, v_dst, r);
+            for (int r = 0; r < kRounds; ++r) dma_round<false>(p, window_desc<false>(p, b, h, h), k_dst, v_dst, r, 0);
         } else {
 #pragma unroll
             for (int k = 0; k < kKC; ++k) {
@@ -714,48 +714,68 @@ struct Stage<T, NT, true> {
     //    V, which lies p.kv_delta elements after K; piece 12 pads the record
     //    and reloads piece 0).  The last load may run past the last record
     //    into the buffer's padding.
+    // Buffer descriptors of one window's K and V rows (records: K and V
+    // from K's base, V kv_delta elements after K), built once per window.
+    struct WindowDesc {
+        u32x4 k, v;
+    };
+    template <bool kRecs>
+    static __device__ __forceinline__ WindowDesc window_desc(const Params& p, int b, int h, int h0) {
+        const int N = p.N;
+        if constexpr (!kRecs) {
+            return {desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N),
+                    desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N)};
+        } else {
+            const u32x4 d = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N,
+                                          p.kv_delta + 16 * kHeadsPerWg);
+            return {d, d};
+        }
+    }
+    // Records: the lane's byte offset of round r's load, the same for every
+    // window (it depends on the wave, the round and the lane only).
+    template <bool kPaired>
+    static __device__ __forceinline__ int rec_voff(const Params& p, int r) {
+        const int N = p.N;
+        const int lane = threadIdx.x & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
+        const int j = min(wave + kWaves * kHeadsPerWg * r, rec_loads(NT) - 1);  // (unused past the last)
+        const int c = 64 * j + lane;
+        const int n = c / 13;  // record n holds token key_of(n)
+        const int piece = c - 13 * n;
+        const int part = piece < 6 ? 8 * piece : (piece < 12 ? p.kv_delta + 8 * (piece - 6) : 0);
+        return (min(key_of<NT, kPaired>(n), N - 1) * static_cast<int>(p.ks[2]) + part) * static_cast<int>(sizeof(T));
+    }
+
     template <bool kRecs, bool kPaired = false>
-    static __device__ __forceinline__ void dma_round(const Params& p, int b, int h, int h0, T* k_dst, T* v_dst,
-                                                     int r) {
+    static __device__ __forceinline__ void dma_round(const Params& p, const WindowDesc& wd, T* k_dst, T* v_dst,
+                                                     int r, int voff) {
         static_assert(kDma, "LDS-DMA staging");
         const int N = p.N;
         constexpr int es = sizeof(T);
         const int lane = threadIdx.x & 63;
-        const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
         typedef __attribute__((address_space(3))) T LdsT;
         const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
-        const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
         if constexpr (!kRecs) {
+            (void)voff;
+            const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
+            const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
             const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
             const int row0 = 32 * (4 * r + wave);
             if (row0 < kRows) {  // wave-uniform
-                const u32x4 kd = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N);
-                const u32x4 vd = desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N);
                 // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15);
                 // LDS row u holds key key_of(u)
                 const int nk = min(key_of<NT, kPaired>(row0 + ((lane >> 5) << 4) + (lane & 15)), N - 1);
                 const int hk = ((lane >> 4) & 1) * 8;
-                dma16(kd, kl + row0 * 32, (nk * ks2 + hk) * es);
+                dma16(wd.k, kl + row0 * 32, (nk * ks2 + hk) * es);
                 const int nv = min(key_of<NT, kPaired>(row0 + (lane >> 1)), N - 1);
-                dma16(vd, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
+                dma16(wd.v, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
             }
         } else {
             static_assert(kRows == rec_rows(NT), "record rows");
             (void)v_dst;
-            (void)vl;
-            (void)vs2;
-            const int kvd = p.kv_delta;
             const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
             const int j = wave + kWaves * kHeadsPerWg * r;  // wave-uniform
-            if (j < rec_loads(NT)) {
-                const u32x4 d = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N,
-                                              kvd + 16 * kHeadsPerWg);
-                const int c = 64 * j + lane;
-                const int n = c / 13;  // record n holds token key_of(n)
-                const int piece = c - 13 * n;
-                const int part = piece < 6 ? 8 * piece : (piece < 12 ? kvd + 8 * (piece - 6) : 0);
-                dma16(d, kl + j * 1024, (min(key_of<NT, kPaired>(n), N - 1) * ks2 + part) * es);
-            }
+            if (j < rec_loads(NT)) dma16(wd.k, kl + j * 1024, voff);
         }
     }
 
@@ -978,6 +998,15 @@ __device__ __forceinline__ float xmax32(float m) {
 constexpr float kOffsetTarget = 7.0f;     // log2 of the row sum aimed at
 constexpr float kRowSumLimit = 32768.0f;  // row sums (hence every P) stay below 2^15
 
+// LDS-DMA rounds per wave with token records (1 otherwise: an array size).
+template <typename St, bool kRecs>
+constexpr int kRecRounds() {
+    if constexpr (kRecs)
+        return St::template dma_rounds<true>();
+    else
+        return 1;
+}
+
 // The next window's LDS-DMA rounds, issued from inside a window's compute:
 // attend_offset spreads them over its tile pairs, so that a workgroup's
 // loads reach the memory pipeline a few at a time while it computes instead
@@ -986,12 +1015,13 @@ template <typename T, typename St, bool kRecs, bool kPaired>
 struct DmaIssuer {
     static constexpr int kRounds = St::template dma_rounds<kRecs>();
     const Params* p;
-    int b, h, h0;
+    typename St::WindowDesc wd;  // the next window's descriptors
     T* k_dst;
     T* v_dst;
-    bool on;  // a next window exists (wave-uniform)
+    const int* voff;  // records: the lane's offset per round
+    bool on;          // a next window exists (wave-uniform)
     __device__ __forceinline__ void operator()(int r) const {
-        if (on) St::template dma_round<kRecs, kPaired>(*p, b, h, h0, k_dst, v_dst, r);
+        if (on) St::template dma_round<kRecs, kPaired>(*p, wd, k_dst, v_dst, r, kRecs ? voff[r] : 0);
     }
 };
 struct NoIssue {
@@ -1567,12 +1597,19 @@ swin_attention_d16_kernel(const Params p) {
     // (all at once here and for waves without a strip, spread over the
     // compute of the previous window otherwise)
     constexpr bool kSpread = kVec && v_row_major<T>();  // Stage<T, NT, true>::kDma
+    // records: the lane's load offsets per round, the same for every window
+    int rec_off[kRecs ? kRecRounds<St, kRecs>() : 1];
+    if constexpr (kRecs) {
+#pragma unroll
+        for (int r = 0; r < kRecRounds<St, kRecs>(); ++r) rec_off[r] = St::template rec_voff<kPaired>(p, r);
+    }
     auto stage_load = [&](int bw, int sb) {
         if constexpr (kSpread) {
             st.load_q(p, bw, h, q0);
+            const auto wd = St::template window_desc<kRecs>(p, bw, h, h0);
 #pragma unroll
             for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r)
-                St::template dma_round<kRecs, kPaired>(p, bw, h, h0, k_lds[sb], vt_lds[sb], r);
+                St::template dma_round<kRecs, kPaired>(p, wd, k_lds[sb], vt_lds[sb], r, kRecs ? rec_off[r] : 0);
         } else {
             st.load(p, bw, h, q0, k_lds[sb], vt_lds[sb]);
         }
@@ -1613,8 +1650,8 @@ swin_attention_d16_kernel(const Params p) {
         }
         const auto issue = [&]() {
             if constexpr (kSpread)
-                return DmaIssuer<T, St, kRecs, kPaired>{&p, b_next, h, h0, k_lds[buf ^ 1], vt_lds[buf ^ 1],
-                                                         i + 1 < i1};
+                return DmaIssuer<T, St, kRecs, kPaired>{&p, St::template window_desc<kRecs>(p, b_next, h, h0),
+                                                         k_lds[buf ^ 1], vt_lds[buf ^ 1], rec_off, i + 1 < i1};
             else
                 return NoIssue{};
         }();
