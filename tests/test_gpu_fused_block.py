@@ -113,6 +113,48 @@ def test_window_proj_matches_oracle(oracle, dev, case, cdt):
     _compare(got, want, cdt, f"window_proj {name}")
 
 
+@pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+@pytest.mark.parametrize("C,n_out", [(16, 16), (32, 48), (48, 48), (64, 64), (48, 16), (16, 64)])
+@pytest.mark.parametrize("dims", [(1, 9, 10, 11), (3, 9, 9, 9), (1, 2, 3, 3)], ids=["990tok", "2187tok", "18tok"])
+def test_window_proj_register_path(oracle, dev, dims, C, n_out, cdt):
+    """2-byte types with C and n_out at most 64 take the register-resident
+    kernel (weights in registers, permuted contraction and feature order,
+    16-token tiles): token counts that leave a partial last tile, fewer
+    tiles than waves, and n_out != C."""
+    B, D, H, W = dims
+    ws, ss = (7, 7, 7), (3, 3, 3)
+    Dp, Hp, Wp = (-(-n // k) * k for n, k in zip((D, H, W), ws))
+    nwin = B * (Dp // 7) * (Hp // 7) * (Wp // 7)
+    win = seeded((nwin, 343, C), torch.float32, 58).to(cdt)
+    w = (seeded((n_out, C), torch.float32, 59) / C ** 0.5).to(cdt)
+    b = (seeded((n_out,), torch.float32, 60) * 0.1).to(cdt)
+    print(f"window_proj register path {dims} C={C} n_out={n_out} {cdt}", flush=True)
+    got = fused_block.window_proj_3d(win.to(dev), w.to(dev), b.to(dev), B, D, H, W, ws, ss)
+    want = oracle.window_proj(win.double().numpy(), B, D, H, W, ws, ss, w.double().numpy(), b.double().numpy(),
+                              NAME[cdt])
+    assert got.shape == want.shape
+    _compare(got, want, cdt, f"window_proj {dims} C={C} n_out={n_out}")
+    got_nb = fused_block.window_proj_3d(win.to(dev), w.to(dev), None, B, D, H, W, ws, ss)
+    want_nb = oracle.window_proj(win.double().numpy(), B, D, H, W, ws, ss, w.double().numpy(), None, NAME[cdt])
+    _compare(got_nb, want_nb, cdt, "no bias")
+
+
+@pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_window_proj_stage0_full_size(oracle, dev, cdt):
+    """Config-5 stage 0 at full size: [1372, 343, 48] windows -> [4, 48^3, 48],
+    every output token against the oracle (27,648 tiles over several steps
+    per wave)."""
+    B, D, C, ws, ss = 4, 48, 48, (7, 7, 7), (3, 3, 3)
+    win = seeded((B * 343, 343, C), torch.float32, 61).to(cdt)
+    w = (seeded((C, C), torch.float32, 62) / C ** 0.5).to(cdt)
+    b = (seeded((C,), torch.float32, 63) * 0.1).to(cdt)
+    print(f"window_proj stage 0 full size {cdt}", flush=True)
+    got = fused_block.window_proj_3d(win.to(dev), w.to(dev), b.to(dev), B, D, D, D, ws, ss)
+    want = oracle.window_proj(win.double().numpy(), B, D, D, D, ws, ss, w.double().numpy(), b.double().numpy(),
+                              NAME[cdt])
+    _compare(got, want, cdt, "window_proj stage 0")
+
+
 def test_many_tiles_uneven_feature_chunks(oracle, dev):
     """Over 1024 token tiles (no feature split across the grid) and 208
     output features: two LDS chunks (192 + 16), so three of the four waves
