@@ -85,6 +85,34 @@ def _events_time(fn, iters):
     return s.elapsed_time(e) / iters
 
 
+_BUSY = {}
+
+
+def _settle_clock(dev, seconds=0.15):
+    """Keep the GPU busy for `seconds` with long torch matmuls (no kernel of
+    this package, few dispatches in a profiler's records).  The shader clock
+    ramps up over the first tens of milliseconds of load and drops while the
+    host prepares inputs, so a kernel timed right after host-side work would
+    otherwise be timed partly at a lower clock."""
+    import torch
+
+    busy = _BUSY.get(str(dev))
+    if busy is None:
+        busy = _BUSY[str(dev)] = torch.full((8192, 8192), 1e-3, dtype=torch.float16, device=dev)
+    end = time.perf_counter() + seconds
+    while time.perf_counter() < end:
+        for _ in range(4):
+            torch.matmul(busy, busy)
+        torch.cuda.synchronize()
+
+
+def _steady_time(fn, warmup, iters, dev):
+    """_events_time after a clock settle and `warmup` untimed calls."""
+    _settle_clock(dev)
+    _events_time(fn, warmup)
+    return _events_time(fn, iters)
+
+
 def seeded(shape, dtype, seed):
     import torch
 
@@ -119,11 +147,9 @@ def bench_partition(args, dev):
         w = crumpet_amd.fused_shift_partition_3d(xs[i % R], ws, ss)
         crumpet_amd.fused_unshift_unpartition_3d(w, B, D, H, W, C, ws, ss)
 
-    for fn in (part, unpart, step):
-        _events_time(fn, args.warmup)
-    t_part = _events_time(part, args.steps)
-    t_unpart = _events_time(unpart, args.steps)
-    t_step = _events_time(step, args.steps)
+    t_part = _steady_time(part, args.warmup, args.steps, dev)
+    t_unpart = _steady_time(unpart, args.warmup, args.steps, dev)
+    t_step = _steady_time(step, args.warmup, args.steps, dev)
     return dict(t_part=t_part, t_unpart=t_unpart, t_step=t_step)
 
 
@@ -136,8 +162,7 @@ def bench_mask(args, dev):
     def mk(i):
         ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
 
-    _events_time(mk, args.warmup)
-    return _events_time(mk, args.steps)
+    return _steady_time(mk, args.warmup, args.steps, dev)
 
 
 def c3_inputs(dev, sets):
@@ -186,10 +211,8 @@ def bench_attention(args, dev):
         fused_swin_attention_shifted(t[0], t[1], t[2], bias, (C3["D"],) * 3, (7, 7, 7), (3, 3, 3),
                                      0.25, ovs[i % R])
 
-    _events_time(attn, args.warmup)
-    t_attn = _events_time(attn, args.steps)
-    _events_time(attn_shifted, args.warmup)
-    t_shift = _events_time(attn_shifted, args.steps)
+    t_attn = _steady_time(attn, args.warmup, args.steps, dev)
+    t_shift = _steady_time(attn_shifted, args.warmup, args.steps, dev)
     res = dict(t_attn=t_attn, t_shift=t_shift)
 
     # accuracy on a sample of windows vs fp32 torch (GPU) of the same inputs
@@ -252,10 +275,8 @@ def bench_attention_wide(args, dev):
         fused_swin_attention_windows(t[0], t[1], t[2], bias, mask, bnd, 0.25, ovs[i % R])
 
     steps = max(5, args.steps // 4)
-    _events_time(shifted, 3)
-    res = {"t_shift": _events_time(shifted, steps)}
-    _events_time(tensor, 3)
-    res["t_tensor"] = _events_time(tensor, steps)
+    res = {"t_shift": _steady_time(shifted, 3, steps, dev)}
+    res["t_tensor"] = _steady_time(tensor, 3, steps, dev)
     t = views[0]
     idx = torch.arange(0, B, 7, device=dev)
     qf, kf, vf = (t[j][idx].float() for j in range(3))
@@ -330,8 +351,7 @@ def bench_blocks(args, dev):
                                              o.view(nwin, N, H, 16).permute(0, 2, 1, 3))
                 crumpet_amd.fused_unshift_unpartition_3d(o, B, dim, dim, dim, C, ws, ss)
 
-            _events_time(step, args.warmup)
-            ms = _events_time(step, args.steps)
+            ms = _steady_time(step, args.warmup, args.steps, dev)
             # the same three launches replayed as one HIP graph (no host launch overhead)
             cap = torch.cuda.Stream()
             cap.wait_stream(torch.cuda.current_stream())
@@ -341,8 +361,7 @@ def bench_blocks(args, dev):
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=cap):
                 step(0)
-            _events_time(lambda i: graph.replay(), args.warmup)
-            ms_graph = _events_time(lambda i: graph.replay(), args.steps)
+            ms_graph = _steady_time(lambda i: graph.replay(), args.warmup, args.steps, dev)
             del graph
             tokens = B * dim ** 3
             part_bytes = 2 * tokens * C * x.element_size()
@@ -400,8 +419,7 @@ def bench_fused_block(args, dev):
             def step(i):
                 with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
                     fn()
-            _events_time(step, args.warmup)
-            return _events_time(step, max(10, args.steps // 4))
+            return _steady_time(step, args.warmup, max(10, args.steps // 4), dev)
 
         t_eager = run(lambda: blk.forward_part1(x, m_eager))
         assert crumpet_amd.patch_monai_swin_unetr()
@@ -434,10 +452,9 @@ def bench_fused_block(args, dev):
         f_qkv = lambda i: ops.window_qkv_3d(qkv_outs[i % 2], xs[i % 2], nrm.weight, nrm.bias, nrm.eps, True,
                                             w_qkv, b_qkv, *ws, *ss)
         f_proj = lambda i: ops.window_proj_3d(ys[i % 2], wins[i % 2], w_p, b_p, *ws, *ss)
-        _events_time(f_qkv, args.warmup)  # first touches of the fresh buffers stay untimed
-        t_qkv = _events_time(f_qkv, args.steps)
-        _events_time(f_proj, args.warmup)
-        t_proj = _events_time(f_proj, args.steps)
+        # (the warm-up calls keep the first touches of the fresh buffers untimed)
+        t_qkv = _steady_time(f_qkv, args.warmup, args.steps, dev)
+        t_proj = _steady_time(f_proj, args.warmup, args.steps, dev)
         qkv_bytes = x.numel() * 4 + qkv_outs[0].numel() * 2
         proj_bytes = wins[0].numel() * 2 + ys[0].numel() * 2
         gq = qkv_bytes / (t_qkv * 1e-3) / 1e9
@@ -676,21 +693,8 @@ def profile_run(dev):
     ops = torch.ops.crumpet_ops
     n = 20
     times = {}
-    busy = torch.full((8192, 8192), 1e-3, dtype=torch.float16, device=dev)
-
-    def settle(seconds=0.15):
-        # The shader clock ramps up over the first tens of milliseconds of
-        # load and drops while the host prepares inputs: keep the GPU busy
-        # with a few long torch matmuls (no kernel of this package, few
-        # dispatches in the profiler's records) first.
-        end = time.perf_counter() + seconds
-        while time.perf_counter() < end:
-            for _ in range(4):
-                torch.matmul(busy, busy)
-            torch.cuda.synchronize()
-
     def timed(name, fn):
-        settle()
+        _settle_clock(dev)
         for i in range(2):  # the first launches load the code object
             fn(i)
         times[name] = round(_events_time(fn, n) * 1e3, 2)

@@ -31,10 +31,12 @@
 // L2-resident weight matrix.  The MFMA result layout gives each lane 4
 // consecutive output features of one token; they go to an LDS output chunk
 // that the workgroup writes back as consecutive 16-byte vectors.
-// window_proj in a 2-byte type with C and n_out at most 64 (stage 0) takes
-// window_proj_stream_kernel instead: independent persistent waves with the
-// weights in registers (74% of HBM at stage 0 against 60% for the tiled
-// kernel, whose workgroups drain the memory queue at every barrier).
+// With a 2-byte compute type and small C (stage 0), window_proj (C and
+// n_out at most 64) and window_qkv (n_out = 3 C, C at most 48) take
+// window_proj_stream_kernel / window_qkv_stream_kernel instead: independent
+// persistent waves with the weights in registers (stage 0: 74% and 77% of
+// HBM against 60% and 69% for the tiled kernels, whose workgroups drain the
+// memory queue at every barrier).
 //
 // Numerics: LayerNorm in fp32 (two passes: mean, then the mean of squared
 // deviations; biased variance, as torch), the normalised value rounded once
@@ -641,6 +643,160 @@ window_proj_stream_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const 
     }
 }
 
+// window_qkv for 2-byte compute types with n_out = 3 C and C at most 48
+// (stage 0 of Swin UNETR: 48 -> 144): the weight matrix, its bias and the
+// LayerNorm parameters stay in registers; waves run independently over
+// 16-token tiles of the window-ordered output, as in
+// window_proj_stream_kernel and with its fragment layout: lane group q holds
+// channels [4*KS*q, 4*KS*(q+1)) of its token, so the LayerNorm statistics
+// are sums over the token's 4 lanes (lanes col + 16 q), and features
+// [4*FT*q, 4*FT*(q+1)) of the result.  The tile's 16 output rows are
+// consecutive; they leave through the wave's LDS slice as 16-byte vectors.
+template <typename Tx, typename Tc, int KS, int kDepth>
+__global__ void __launch_bounds__(kThreads)
+window_qkv_stream_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln_w, const void* ln_b,
+                         int32_t ln_dtype, int32_t normalize, float eps, const Tc* __restrict__ w,
+                         const Tc* __restrict__ bias, const WinGeom g, uint32_t tiles) {
+    typedef typename Mma<Tc>::x4 X4;
+    typedef Tc T4 __attribute__((ext_vector_type(4)));
+    typedef Tx Tx4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t V16 __attribute__((ext_vector_type(4)));
+    constexpr int C = 16 * KS, FT = 3 * KS, NO = 16 * FT;
+    constexpr int kWavesPerWg = kThreads / 64;
+    constexpr int kPad = 8;
+    constexpr int kOutVecs = 16 * NO / 8;
+    __shared__ __attribute__((aligned(16))) Tc out_lds[kWavesPerWg][16 * (NO + kPad)];
+    // fp32 bias and LayerNorm parameters, shared by the workgroup's waves
+    // (read per tile: in registers they would cost a wave per SIMD)
+    __shared__ __attribute__((aligned(16))) float par_lds[NO + 2 * C];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int q = lane >> 4;
+    const uint32_t wgs = gridDim.x;  // a multiple of 8
+    const uint32_t wg = (blockIdx.x & 7u) * (wgs >> 3) + (blockIdx.x >> 3);
+    const uint32_t waves = wgs * kWavesPerWg;
+    const uint32_t L = wg * kWavesPerWg + wave;
+
+    for (int i = threadIdx.x; i < (NO + 2 * C) / 4; i += kThreads) {
+        f32x4 v;
+        if (4 * i < NO)
+            v = bias ? load4(bias + 4 * i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        else if (4 * i < NO + C)
+            v = load_param4(ln_w, ln_dtype, 4 * i - NO, 1.0f);
+        else
+            v = load_param4(ln_b, ln_dtype, 4 * i - NO - C, 0.0f);
+        *reinterpret_cast<f32x4*>(&par_lds[4 * i]) = v;
+    }
+    X4 wf[FT][KS];
+#pragma unroll
+    for (int ft = 0; ft < FT; ++ft) {
+        const Tc* wr = w + (4 * FT * (col >> 2) + 4 * ft + (col & 3)) * C + 4 * KS * q;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) wf[ft][kk] = *reinterpret_cast<const X4*>(wr + 4 * kk);
+    }
+    __syncthreads();  // par_lds is written (every wave passes here once)
+    const float* b_lds = par_lds + 4 * FT * q;
+    const float* gm_lds = par_lds + NO + 4 * KS * q;
+    const float* bt_lds = par_lds + NO + C + 4 * KS * q;
+
+    struct Raw {
+        Tx4 v[KS];
+        bool pad;
+    };
+    // the lane's channels of window-ordered token t (tiles clamped to the
+    // last, so that the loads are unconditional; padding reads row 0)
+    auto load_tile = [&](uint32_t t, Raw& r) {
+        const uint32_t tok = min(t, tiles - 1) * 16 + col;
+        const uint32_t row = tok < g.tokens ? token_row(tok, g) : kPadRow;
+        r.pad = row == kPadRow;
+        const Tx* src = x + int64_t(r.pad ? 0u : row) * C + 4 * KS * q;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) r.v[kk] = *reinterpret_cast<const Tx4*>(src + 4 * kk);
+    };
+    auto wave_sync = []() {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    auto run_tile = [&](uint32_t t, const Raw& r) {
+        f32x4 v[KS];
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[kk][e] = r.pad ? 0.0f : to_f32(r.v[kk][e]);
+        if (normalize) {
+            float sm = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) sm += (v[kk][0] + v[kk][1]) + (v[kk][2] + v[kk][3]);
+            sm += __shfl_xor(sm, 16);
+            sm += __shfl_xor(sm, 32);
+            const float mean = sm / static_cast<float>(C);
+            float qs = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float dv = v[kk][e] - mean;
+                    qs = __builtin_fmaf(dv, dv, qs);
+                }
+            qs += __shfl_xor(qs, 16);
+            qs += __shfl_xor(qs, 32);
+            const float rstd = rsqrtf(qs / static_cast<float>(C) + eps);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                const f32x4 gm = *reinterpret_cast<const f32x4*>(gm_lds + 4 * kk);
+                const f32x4 bt = *reinterpret_cast<const f32x4*>(bt_lds + 4 * kk);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[kk][e] = r.pad ? 0.0f : __builtin_fmaf((v[kk][e] - mean) * rstd, gm[e], bt[e]);
+            }
+        }
+        X4 xf[KS];
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xf[kk][e] = static_cast<Tc>(v[kk][e]);
+        Tc* ol = out_lds[wave];
+        wave_sync();  // the previous tile's vectors have been read
+#pragma unroll
+        for (int ft = 0; ft < FT; ++ft) {
+            f32x4 acc = *reinterpret_cast<const f32x4*>(b_lds + 4 * ft);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) acc = Mma<Tc>::step(wf[ft][kk], xf[kk], acc);
+            T4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = static_cast<Tc>(acc[e]);
+            *reinterpret_cast<T4*>(&ol[col * (NO + kPad) + 4 * FT * q + 4 * ft]) = o;
+        }
+        wave_sync();
+        const uint32_t t16 = t * 16;
+#pragma unroll
+        for (int it = 0; it < (kOutVecs + 63) / 64; ++it) {
+            const int i = lane + 64 * it;
+            const int tok = i / (NO / 8);
+            const int part = i - tok * (NO / 8);
+            if (i < kOutVecs && t16 + tok < g.tokens)
+                __builtin_nontemporal_store(*reinterpret_cast<const V16*>(&ol[tok * (NO + kPad) + 8 * part]),
+                                            reinterpret_cast<V16*>(out + int64_t(t16 + tok) * NO + 8 * part));
+        }
+    };
+
+    Raw raw[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load_tile(L + d * waves, raw[d]);
+    for (uint32_t t0 = L; t0 < tiles; t0 += kDepth * waves) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            const uint32_t t = t0 + d * waves;
+            if (t < tiles) {  // wave-uniform
+                run_tile(t, raw[d]);
+                load_tile(t + kDepth * waves, raw[d]);
+            }
+        }
+    }
+}
+
 int elem_size(int32_t dtype) {
     switch (dtype) {
         case CRUMPET_DTYPE_F32: return 4;
@@ -795,6 +951,52 @@ bool proj_streams(int32_t dtype, int64_t C, int64_t n_out) {
     return elem_size(dtype) == 2 && C <= 64 && n_out <= 64;
 }
 
+constexpr int kQkvStreamDepth = 1;
+constexpr uint32_t kQkvStreamWorkgroups = 512;
+
+bool qkv_streams(int32_t dtype, int64_t C, int64_t n_out) {
+    return elem_size(dtype) == 2 && C <= 48 && n_out == 3 * C;
+}
+
+// Grid of a streaming kernel: the fewest steps that `cap` workgroups allow,
+// then the fewest workgroups (a multiple of 8, one per XCD) that take every
+// tile in that many steps, so that the last step is nearly full for every
+// wave.
+dim3 stream_grid(uint32_t tiles, uint32_t cap) {
+    constexpr uint32_t kWaves = kThreads / 64;
+    const uint32_t steps = std::max(1u, (tiles + cap * kWaves - 1) / (cap * kWaves));
+    const uint32_t wgs = (tiles + steps * kWaves - 1) / (steps * kWaves);
+    return dim3(std::max(8u, (wgs + 7) / 8 * 8));
+}
+
+template <typename Tx, typename Tc>
+void launch_qkv_stream(int KS, hipStream_t s, void* out, const void* x, const void* ln_w, const void* ln_b,
+                       int32_t ln_dtype, int32_t normalize, float eps, const void* w, const void* bias,
+                       const WinGeom& g) {
+    const uint32_t tiles = (g.tokens + 15) / 16;
+    const dim3 grid = stream_grid(tiles, kQkvStreamWorkgroups);
+#define CRUMPET_QKV_STREAM(K)                                                                          \
+    hipLaunchKernelGGL((window_qkv_stream_kernel<Tx, Tc, K, kQkvStreamDepth>), grid, dim3(kThreads), 0, s, \
+                       static_cast<Tc*>(out), static_cast<const Tx*>(x), ln_w, ln_b, ln_dtype, normalize, eps,  \
+                       static_cast<const Tc*>(w), static_cast<const Tc*>(bias), g, tiles)
+    switch (KS) {
+        case 1: CRUMPET_QKV_STREAM(1); break;
+        case 2: CRUMPET_QKV_STREAM(2); break;
+        default: CRUMPET_QKV_STREAM(3); break;
+    }
+#undef CRUMPET_QKV_STREAM
+}
+
+template <typename Tx>
+void launch_qkv_stream_x(int32_t dtype, int KS, hipStream_t s, void* out, const void* x, const void* ln_w,
+                         const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps, const void* w,
+                         const void* bias, const WinGeom& g) {
+    if (dtype == CRUMPET_DTYPE_F16)
+        launch_qkv_stream<Tx, _Float16>(KS, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
+    else
+        launch_qkv_stream<Tx, __bf16>(KS, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
+}
+
 template <typename Tc, int KS>
 void launch_proj_stream_ks(int FT, dim3 grid, hipStream_t s, void* y, const void* win, const void* w,
                            const void* bias, const WinGeom& g, uint32_t tiles) {
@@ -815,13 +1017,7 @@ template <typename Tc>
 void launch_proj_stream(int KS, int FT, hipStream_t s, void* y, const void* win, const void* w,
                         const void* bias, const WinGeom& g) {
     const uint32_t tiles = (g.vtokens + 15) / 16;
-    // the fewest steps that kStreamWorkgroups allow, then the fewest
-    // workgroups (a multiple of 8, one per XCD) that take every tile in that
-    // many steps: the last step is then nearly full for every wave
-    constexpr uint32_t kWaves = kThreads / 64;
-    const uint32_t steps = (tiles + kStreamWorkgroups * kWaves - 1) / (kStreamWorkgroups * kWaves);
-    const uint32_t wgs = (tiles + steps * kWaves - 1) / (steps * kWaves);
-    const dim3 grid(std::max(8u, (wgs + 7) / 8 * 8));
+    const dim3 grid = stream_grid(tiles, kStreamWorkgroups);
     switch (KS) {
         case 1: launch_proj_stream_ks<Tc, 1>(FT, grid, s, y, win, w, bias, g, tiles); break;
         case 2: launch_proj_stream_ks<Tc, 2>(FT, grid, s, y, win, w, bias, g, tiles); break;
@@ -865,6 +1061,19 @@ extern "C" int crumpet_window_qkv_3d(void* out, int32_t dtype, const void* x, in
          reinterpret_cast<uintptr_t>(ln_weight) | reinterpret_cast<uintptr_t>(ln_bias)) % 16 != 0)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: pointers must be 16-byte aligned", what);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    if (qkv_streams(dtype, C, n_out)) {
+        const int KS = static_cast<int>(C / 16);
+        if (x_dtype == CRUMPET_DTYPE_F32)
+            launch_qkv_stream_x<float>(dtype, KS, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps, weight,
+                                       bias, g);
+        else if (x_dtype == CRUMPET_DTYPE_F16)
+            launch_qkv_stream_x<_Float16>(dtype, KS, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                                          weight, bias, g);
+        else
+            launch_qkv_stream_x<__bf16>(dtype, KS, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                                        weight, bias, g);
+        return check_launch(what);
+    }
     if (x_dtype == CRUMPET_DTYPE_F32)
         launch_qkv_x<float>(dtype, grid, lds, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps, weight,
                             bias, ts, g);

@@ -113,6 +113,58 @@ def test_window_proj_matches_oracle(oracle, dev, case, cdt):
     _compare(got, want, cdt, f"window_proj {name}")
 
 
+@pytest.mark.parametrize("dts", DTYPES[:2] + DTYPES[3:], ids=lambda d: f"{NAME[d[0]]}-{NAME[d[1]]}")
+@pytest.mark.parametrize("C", [16, 32, 48])
+@pytest.mark.parametrize("dims", [(1, 9, 10, 11), (1, 2, 3, 3)], ids=["9x10x11", "2x3x3"])
+def test_window_qkv_register_path(oracle, dev, dims, C, dts):
+    """2-byte compute types with n_out = 3 C and C at most 48 take the
+    register-resident kernel (LayerNorm statistics over the 4 lanes of a
+    token, permuted contraction and feature order, 16-token tiles): a
+    partial last tile, fewer tiles than waves, LayerNorm off, and LayerNorm
+    parameters in the input's dtype."""
+    B, D, H, W = dims
+    xdt, cdt = dts
+    ws, ss = (7, 7, 7), (3, 3, 3)
+    x = (seeded((B, D, H, W, C), torch.float32, 64) * 2.0 + 0.5).to(xdt)
+    gw = seeded((C,), torch.float32, 65) * 0.5 + 1.0
+    gb = seeded((C,), torch.float32, 66) * 0.1
+    w = (seeded((3 * C, C), torch.float32, 67) / C ** 0.5).to(cdt)
+    b = (seeded((3 * C,), torch.float32, 68) * 0.1).to(cdt)
+    print(f"window_qkv register path {dims} C={C} {xdt}->{cdt}", flush=True)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    xn, wn, bn = x.double().numpy(), w.double().numpy(), b.double().numpy()
+    got = fused_block.window_qkv_3d(xd, wd, bd, ws, ss, gw.to(dev), gb.to(dev), 1e-5, True, cdt)
+    want = oracle.window_qkv(xn, ws, ss, wn, bn, gw.double().numpy(), gb.double().numpy(), 1e-5, True, NAME[cdt])
+    assert got.shape == want.shape
+    _compare(got, want, cdt, f"window_qkv {dims} C={C}")
+    got = fused_block.window_qkv_3d(xd, wd, None, ws, ss, normalize=False, dtype=cdt)
+    want = oracle.window_qkv(xn, ws, ss, wn, None, normalize=False, dtype=NAME[cdt])
+    _compare(got, want, cdt, "no norm, no bias")
+    if xdt != torch.float32:
+        gwx = gw.to(xdt)
+        got = fused_block.window_qkv_3d(xd, wd, bd, ws, ss, gwx.to(dev), None, 1e-6, True, cdt)
+        want = oracle.window_qkv(xn, ws, ss, wn, bn, gwx.double().numpy(), None, 1e-6, True, NAME[cdt])
+        _compare(got, want, cdt, "LN weight in the input dtype, no LN bias")
+
+
+@pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_window_qkv_stage0_full_size(oracle, dev, cdt):
+    """Config-5 stage 0 at full size: fp32 [4, 48^3, 48] -> [1372, 343, 144],
+    every window-ordered token (padding included) against the oracle."""
+    B, D, C, ws, ss = 4, 48, 48, (7, 7, 7), (3, 3, 3)
+    x = seeded((B, D, D, D, C), torch.float32, 69) * 1.5 + 0.25
+    gw = seeded((C,), torch.float32, 70) * 0.5 + 1.0
+    gb = seeded((C,), torch.float32, 71) * 0.1
+    w = (seeded((3 * C, C), torch.float32, 72) / C ** 0.5).to(cdt)
+    b = (seeded((3 * C,), torch.float32, 73) * 0.1).to(cdt)
+    print(f"window_qkv stage 0 full size {cdt}", flush=True)
+    got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), b.to(dev), ws, ss, gw.to(dev), gb.to(dev), 1e-5, True,
+                                    cdt)
+    want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), b.double().numpy(),
+                             gw.double().numpy(), gb.double().numpy(), 1e-5, True, NAME[cdt])
+    _compare(got, want, cdt, "window_qkv stage 0")
+
+
 @pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
 @pytest.mark.parametrize("C,n_out", [(16, 16), (32, 48), (48, 48), (64, 64), (48, 16), (16, 64)])
 @pytest.mark.parametrize("dims", [(1, 9, 10, 11), (3, 9, 9, 9), (1, 2, 3, 3)], ids=["990tok", "2187tok", "18tok"])
