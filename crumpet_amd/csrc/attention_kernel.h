@@ -32,9 +32,6 @@
 //   whole 128-byte lines.  Otherwise each thread holds its share in
 //   registers and stores it after the compute (fp32 keeps V transposed;
 //   2-byte types keep V row-major and read V^T with the LDS transpose read).
-//   With a mask tensor the 2-byte DMA kernels use the paired key order
-//   (key_of), in which a lane's mask and bias values of two tiles are one
-//   load.
 //
 //   In region mode the windows are visited grouped by type (which axes the
 //   window is last on; at most 8 types).  The shifted-window mask of a window
@@ -212,32 +209,6 @@ constexpr int first_last_tile(int NT) {
 // N - 1 (the fp32-operand kernel's mask reads those element by element).
 __device__ __forceinline__ bool holds_last_key(int k0, int nk, int row, int N) {
     return row == N - 1 && k0 <= N - 1 && k0 + nk - 1 >= N - 1;
-}
-
-// Key order.  Tile t's row 4g + r (lane group g's key r of the tile) holds
-// key 16t + 4g + r, except in the paired order (kPaired): in each full pair
-// of tiles (2p, 2p + 1), row 4g + r of tile 2p + j holds key 32p + 8g +
-// 4j + r, so that the 8 keys a lane holds across the pair are consecutive
-// (one load of its mask or bias values per pair instead of two, over half
-// the cache lines).  A lone last tile keeps the plain order.  Attention
-// sums over keys: K, V, the bias and the mask only have to agree on the
-// order.
-template <int NT, bool kPaired>
-__device__ __forceinline__ int key_of(int u) {  // u = 16t + 4g + r, any lane slot or LDS row
-    const int t = u >> 4;
-    if (!kPaired || u >= 16 * NT || (t | 1) >= NT) return u;
-    const int i = u & 15;
-    return (u & ~31) + ((i >> 2) << 3) + ((t & 1) << 2) + (i & 3);
-}
-// Keys per lane in the load unit starting at tile t0 (4, or 8 for a full
-// pair in the paired order), and the first of them for lane group g.
-template <int NT, bool kPaired>
-__device__ __forceinline__ constexpr int unit_keys(int t0) {
-    return kPaired && t0 + 1 < NT ? 8 : 4;
-}
-template <int NT, bool kPaired>
-__device__ __forceinline__ int unit_key0(int t0, int g) {
-    return unit_keys<NT, kPaired>(t0) == 8 ? 16 * t0 + 8 * g : 16 * t0 + 4 * g;
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -706,7 +677,7 @@ struct Stage<T, NT, true> {
     // fetches sets the layout.
     //  - One head (h): round r of wave w fills rows 32*(4r + w) .. +31, K in
     //    the kidx tile layout, V as plain 32-byte rows (its transpose reads
-    //    are conflict-free); row u holds key key_of<NT, kPaired>(u).
+    //    are conflict-free); row u holds key u.
     //  - kHeadsPerWg heads (h0 ..): token records (kRecStride elements),
     //    load j = wave + 4 * kHeadsPerWg * r of the workgroup's loads fills
     //    chunks 64j .. 64j + 63: chunk c is token c / 13, piece c % 13 (pieces
@@ -733,20 +704,19 @@ struct Stage<T, NT, true> {
     }
     // Records: the lane's byte offset of round r's load, the same for every
     // window (it depends on the wave, the round and the lane only).
-    template <bool kPaired>
     static __device__ __forceinline__ int rec_voff(const Params& p, int r) {
         const int N = p.N;
         const int lane = threadIdx.x & 63;
         const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6);
         const int j = min(wave + kWaves * kHeadsPerWg * r, rec_loads(NT) - 1);  // (unused past the last)
         const int c = 64 * j + lane;
-        const int n = c / 13;  // record n holds token key_of(n)
+        const int n = c / 13;  // record n holds token n
         const int piece = c - 13 * n;
         const int part = piece < 6 ? 8 * piece : (piece < 12 ? p.kv_delta + 8 * (piece - 6) : 0);
-        return (min(key_of<NT, kPaired>(n), N - 1) * static_cast<int>(p.ks[2]) + part) * static_cast<int>(sizeof(T));
+        return (min(n, N - 1) * static_cast<int>(p.ks[2]) + part) * static_cast<int>(sizeof(T));
     }
 
-    template <bool kRecs, bool kPaired = false>
+    template <bool kRecs>
     static __device__ __forceinline__ void dma_round(const Params& p, const WindowDesc& wd, T* k_dst, T* v_dst,
                                                      int r, int voff) {
         static_assert(kDma, "LDS-DMA staging");
@@ -762,12 +732,11 @@ struct Stage<T, NT, true> {
             const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
             const int row0 = 32 * (4 * r + wave);
             if (row0 < kRows) {  // wave-uniform
-                // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15);
-                // LDS row u holds key key_of(u)
-                const int nk = min(key_of<NT, kPaired>(row0 + ((lane >> 5) << 4) + (lane & 15)), N - 1);
+                // K: chunk l of these two tiles is (tile l/32, dims 8*((l/16)&1), row l&15)
+                const int nk = min(row0 + ((lane >> 5) << 4) + (lane & 15), N - 1);
                 const int hk = ((lane >> 4) & 1) * 8;
                 dma16(wd.k, kl + row0 * 32, (nk * ks2 + hk) * es);
-                const int nv = min(key_of<NT, kPaired>(row0 + (lane >> 1)), N - 1);
+                const int nv = min(row0 + (lane >> 1), N - 1);
                 dma16(wd.v, vl + row0 * 32, (nv * vs2 + (lane & 1) * 8) * es);
             }
         } else {
@@ -799,8 +768,8 @@ struct Stage<T, NT, true> {
 };
 
 // Bias (+ region mask) tiles of one strip, built in registers from the
-// caller's bias tensor: lane (col, g) holds keys key_of<NT, kPairs>(16t +
-// 4g + r) of query qi.  The head's [N, N] bias is read through a buffer
+// caller's bias tensor: lane (col, g) holds keys 16t + 4g + r of query
+// qi.  The head's [N, N] bias is read through a buffer
 // descriptor; keys past N read 0 or the next row and are replaced by -inf
 // (probability exactly 0).  Padded query rows get 0 (never stored).  In
 // region mode a key whose shift-region class differs from the query's on
@@ -810,16 +779,15 @@ struct Stage<T, NT, true> {
 // when the window type changes (at most 8 times per workgroup) or the
 // offsets move, never per window otherwise.
 //
-// A lane's keys of one load unit (a tile, or a pair of tiles in the paired
-// key order) are consecutive in its bias row, so each unit is one load, and
-// all of a wave's loads are issued before any is used (one memory round
-// trip per build).  16-bit rows of an odd row stride start in the middle of
+// A lane's 4 keys of a tile are consecutive in its bias row, so each tile
+// is one load, and all of a wave's loads are issued before any is used (one
+// memory round trip per build).  16-bit rows of an odd row stride start in the middle of
 // a dword and unaligned loads are slow, so those lanes load the dwords
 // around their keys from a dword-aligned offset and shift the halves into
 // place (shift: 0 or 16 bits).  The resource is dword-aligned
 // (aligned_rsrc).  (Bias rows never overlap: the host checks that the row
 // stride is at least N.)
-template <int NT, int kMask, bool kLog2, int kBiasDtype, bool kPaired>
+template <int NT, int kMask, bool kLog2, int kBiasDtype>
 __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_rsrc_t rs, int lead, int N,
                                                int64_t bsd1, int qi, int g, int code, const uint8_t* cls,
                                                float off) {
@@ -839,37 +807,24 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
         cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
         cmask = uint32_t(code) * 0x01010101u;
     }
-    // load units: tiles, or pairs of tiles (a lone last tile on its own)
-    constexpr int kUnits = kPaired ? (NT + 1) / 2 : NT;
-    constexpr int kMaxKeys = kPaired && NT > 1 ? 8 : 4;
-    constexpr int kWords = kEs == 4 ? kMaxKeys : kMaxKeys / 2 + 1;
-    // Two halves of the units, each: all loads, then the conversions (the
-    // raw words of every unit at once would not fit next to the tiles).
-    constexpr int kHalf = (kUnits + 1) / 2;
+    // words per tile: 4 fp32 keys, or the 3 dwords around 4 16-bit keys
+    constexpr int kWords = kEs == 4 ? 4 : 3;
+    // Two halves of the tiles, each: all loads, then the conversions (the
+    // raw words of every tile at once would not fit next to the tiles).
+    constexpr int kHalf = (NT + 1) / 2;
 #pragma unroll
-    for (int u0 = 0; u0 < kUnits; u0 += kHalf) {
+    for (int u0 = 0; u0 < NT; u0 += kHalf) {
         __builtin_amdgcn_sched_barrier(0);
         uint32_t raw[kHalf][kWords];
 #pragma unroll
         for (int u = 0; u < kHalf; ++u) {
-            const int un = u0 + u;
-            if (un >= kUnits) break;
-            const int t0 = kPaired ? 2 * un : un;      // first tile of the unit
-            const int nk = unit_keys<NT, kPaired>(t0);  // keys per lane: 4 or 8
-            const int o = rowb + unit_key0<NT, kPaired>(t0, g) * kEs;
+            const int t = u0 + u;
+            if (t >= NT) break;
+            const int o = rowb + (16 * t + 4 * g) * kEs;
             if constexpr (kEs == 4) {
-#pragma unroll
-                for (int h = 0; h < nk / 4; ++h) {
-                    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, o + 16 * h, 0, 0);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) raw[u][4 * h + i < kWords ? 4 * h + i : kWords - 1] = w[i];
-                }
-            } else if (kMaxKeys == 8 && nk == 8) {
-                // (indices clamped: kWords is 5 whenever a unit has 8 keys)
                 const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rs, o, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) raw[u][i < kWords ? i : kWords - 1] = w[i];
-                raw[u][kWords - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, o + 16, 0, 0);
+                for (int i = 0; i < 4; ++i) raw[u][i] = w[i];
             } else {
                 const u32x3 w = __builtin_amdgcn_raw_buffer_load_b96(rs, o, 0, 0);
 #pragma unroll
@@ -878,52 +833,47 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
         }
 #pragma unroll
         for (int u = 0; u < kHalf; ++u) {
-            const int un = u0 + u;
-            if (un >= kUnits) break;
-            const int t0 = kPaired ? 2 * un : un;
+            const int t = u0 + u;
+            if (t >= NT) break;
+            // one tile at a time: scheduled together, the per-key lane
+            // masks of all tiles would not fit the scalar registers
+            __builtin_amdgcn_sched_barrier(0);
+            const int k4 = 16 * t + 4 * g;  // the tile's 4 keys
+            uint32_t split = 0;  // byte r nonzero: key k4 + r is masked by the region rule
+            if constexpr (kMask == kMaskRegion)
+                split = (*reinterpret_cast<const uint32_t*>(&cls[k4]) ^ cq) & cmask;
+            float v4[4];
+            if constexpr (kEs == 4) {
 #pragma unroll
-            for (int j = 0; j < unit_keys<NT, kPaired>(t0) / 4; ++j) {
-                const int t = t0 + j;
-                // one tile at a time: scheduled together, the per-key lane
-                // masks of all tiles would not fit the scalar registers
-                __builtin_amdgcn_sched_barrier(0);
-                const int k4 = unit_key0<NT, kPaired>(t0, g) + 4 * j;  // the tile's 4 keys
-                uint32_t split = 0;  // byte r nonzero: key k4 + r is masked by the region rule
-                if constexpr (kMask == kMaskRegion)
-                    split = (*reinterpret_cast<const uint32_t*>(&cls[k4]) ^ cq) & cmask;
-                float v4[4];
-                if constexpr (kEs == 4) {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) v4[r] = __uint_as_float(raw[u][4 * j + r]);
-                } else {
-                    const uint32_t hw[2] = {__builtin_amdgcn_alignbit(raw[u][2 * j + 1], raw[u][2 * j], shift),
-                                            __builtin_amdgcn_alignbit(raw[u][2 * j + 2], raw[u][2 * j + 1], shift)};
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const uint32_t bits = (r & 1) ? hw[r >> 1] >> 16 : hw[r >> 1] & 0xffffu;
-                        if constexpr (kBiasDtype == CRUMPET_DTYPE_BF16)
-                            v4[r] = __uint_as_float(bits << 16);
-                        else
-                            v4[r] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-                    }
-                }
+                for (int r = 0; r < 4; ++r) v4[r] = __uint_as_float(raw[u][r]);
+            } else {
+                const uint32_t hw[2] = {__builtin_amdgcn_alignbit(raw[u][1], raw[u][0], shift),
+                                        __builtin_amdgcn_alignbit(raw[u][2], raw[u][1], shift)};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float val = v4[r];
-                    if constexpr (kMask == kMaskRegion) {
-                        if ((split >> (8 * r)) & 0xffu) val += -100.0f;
-                    }
-                    if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
-                    val = row ? val : 0.0f;
-                    bs[t][r] = (k4 + r) < N ? val : -INFINITY;
+                    const uint32_t bits = (r & 1) ? hw[r >> 1] >> 16 : hw[r >> 1] & 0xffffu;
+                    if constexpr (kBiasDtype == CRUMPET_DTYPE_BF16)
+                        v4[r] = __uint_as_float(bits << 16);
+                    else
+                        v4[r] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
                 }
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float val = v4[r];
+                if constexpr (kMask == kMaskRegion) {
+                    if ((split >> (8 * r)) & 0xffu) val += -100.0f;
+                }
+                if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
+                val = row ? val : 0.0f;
+                bs[t][r] = (k4 + r) < N ? val : -INFINITY;
             }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int NT, int kMask, bool kLog2, bool kPaired>
+template <int NT, int kMask, bool kLog2>
 __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, int h, int qi, int g,
                                             int code, const uint8_t* cls, float off) {
     // Re-read the kernel arguments (Params is the kernel's only argument, at
@@ -945,14 +895,11 @@ __device__ __forceinline__ void build_tiles(f32x4 (&bs)[NT], const Params& prm, 
                                         (int64_t(N - 1) * bsd1 + N) * es);
     // uniform: one dtype branch per build, none per tile or element
     if (bias_dtype == CRUMPET_DTYPE_F32)
-        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F32, kPaired>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls,
-                                                                       off);
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F32>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls, off);
     else if (bias_dtype == CRUMPET_DTYPE_BF16)
-        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_BF16, kPaired>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls,
-                                                                       off);
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_BF16>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls, off);
     else
-        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F16, kPaired>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls,
-                                                                       off);
+        build_tiles_es<NT, kMask, kLog2, CRUMPET_DTYPE_F16>(bs, ar.rs, ar.lead, N, bsd1, qi, g, code, cls, off);
 }
 
 
@@ -1011,7 +958,7 @@ constexpr int kRecRounds() {
 // attend_offset spreads them over its tile pairs, so that a workgroup's
 // loads reach the memory pipeline a few at a time while it computes instead
 // of all at the window start (where every wave would stall on issue).
-template <typename T, typename St, bool kRecs, bool kPaired>
+template <typename T, typename St, bool kRecs>
 struct DmaIssuer {
     static constexpr int kRounds = St::template dma_rounds<kRecs>();
     const Params* p;
@@ -1021,7 +968,7 @@ struct DmaIssuer {
     const int* voff;  // records: the lane's offset per round
     bool on;          // a next window exists (wave-uniform)
     __device__ __forceinline__ void operator()(int r) const {
-        if (on) St::template dma_round<kRecs, kPaired>(*p, wd, k_dst, v_dst, r, kRecs ? voff[r] : 0);
+        if (on) St::template dma_round<kRecs>(*p, wd, k_dst, v_dst, r, kRecs ? voff[r] : 0);
     }
 };
 struct NoIssue {
@@ -1029,7 +976,7 @@ struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
 
-template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, bool kPaired, typename Issue>
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, typename Issue>
 __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
                                               const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
                                               int h, int wave, int qi, int col, int g, float& off,
@@ -1066,69 +1013,50 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         mrsrc = ar.rs;
         mvoff = ar.lead + static_cast<int>(qr * p.ms[1] * kMaskBytes);
     }
-    // Mask values by load unit (a tile, or in the paired key order a pair of
-    // tiles: key_of), each lane's keys of a unit consecutive in its row.
+    // Mask values by tile, a lane's 4 keys of a tile consecutive in its row.
     // 2-byte masks: a row of an odd row stride starts in the middle of a
     // dword, and unaligned loads are slow.  Each lane therefore loads the
     // dwords around its keys from a dword-aligned offset (mvoff is the row's,
     // in a dword-aligned resource: aligned_rsrc) and shifts its halves into
-    // place when it uses them (mshift: 0 or 16 bits).  Words per unit: 2-byte
-    // 3 (4 keys) or 5 (8 keys), fp32 4 or 8.
+    // place when it uses them (mshift: 0 or 16 bits).  Words per tile: 2-byte
+    // 3, fp32 4.
     int mshift = 0;
     if constexpr (kUseMask && kMaskBytes == 2) {
         mshift = (mvoff & 2) * 8;
         mvoff &= ~3;
     }
-    constexpr int kMaxKeys = kPaired && NT > 1 ? 8 : 4;
-    constexpr int kMWords = kMaskBytes == 2 ? kMaxKeys / 2 + 1 : kMaxKeys;
+    constexpr int kMWords = kMaskBytes == 2 ? 3 : 4;
     typedef uint32_t MaskWords[kMWords];
-    // the first tile of the load unit holding tile t (compile-time)
-    auto unit_of = [](int t) { return kPaired && (t & 1) ? t - 1 : t; };
-    // the words of the unit starting at tile t
+    // the words of tile t
     auto fetch = [&](int t, MaskWords& w) {
         if constexpr (kUseMask) {
-            const int nk = unit_keys<NT, kPaired>(t);
-            const int k0 = unit_key0<NT, kPaired>(t, g);
-            const int o = mvoff + k0 * kMaskBytes;
+            const int o = mvoff + (16 * t + 4 * g) * kMaskBytes;
             if constexpr (kMaskBytes == 2) {
-                if (kMaxKeys == 8 && nk == 8) {
-                    // (indices clamped: kMWords is 5 whenever a unit has 8 keys)
-                    const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o, 0, 0);
+                const u32x3 v3 = __builtin_amdgcn_raw_buffer_load_b96(mrsrc, o, 0, 0);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) w[r < kMWords ? r : kMWords - 1] = v4[r];
-                    w[kMWords - 1] = __builtin_amdgcn_raw_buffer_load_b32(mrsrc, o + 16, 0, 0);
-                } else {
-                    const u32x3 v3 = __builtin_amdgcn_raw_buffer_load_b96(mrsrc, o, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 3; ++r) w[r] = v3[r];
-                }
+                for (int r = 0; r < 3; ++r) w[r] = v3[r];
             } else {
+                const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o, 0, 0);
 #pragma unroll
-                for (int hh = 0; hh < nk / 4; ++hh) {
-                    const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, o + 16 * hh, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) w[4 * hh + r < kMWords ? 4 * hh + r : kMWords - 1] = v4[r];
-                }
+                for (int r = 0; r < 4; ++r) w[r] = v4[r];
             }
         }
     };
     // accumulator input of tile t: bias (+ region mask) tile with the row
-    // offset, plus the mask tensor's values in log2 units (w: the words of
-    // the unit holding tile t)
+    // offset, plus the mask tensor's values in log2 units (w: tile t's words)
     auto cinit = [&](int t, const MaskWords& w) -> f32x4 {
         f32x4 c = bs[t];
         if constexpr (kUseMask) {
-            const int j = t - unit_of(t);  // the tile's place in its unit
-            uint32_t hw[2] = {0u, 0u};     // 2-byte masks: the 4 keys' halves in place
+            uint32_t hw[2] = {0u, 0u};  // 2-byte masks: the 4 keys' halves in place
             if constexpr (kMaskBytes == 2) {
-                hw[0] = __builtin_amdgcn_alignbit(w[2 * j + 1], w[2 * j], mshift);
-                hw[1] = __builtin_amdgcn_alignbit(w[2 * j + 2], w[2 * j + 1], mshift);
+                hw[0] = __builtin_amdgcn_alignbit(w[1], w[0], mshift);
+                hw[1] = __builtin_amdgcn_alignbit(w[2], w[1], mshift);
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float mv;
                 if constexpr (kMask == kMaskF32)
-                    mv = __uint_as_float(w[4 * j + r]);
+                    mv = __uint_as_float(w[r]);
                 else if constexpr (kMask == kMaskF16)
                     mv = static_cast<float>(
                         __builtin_bit_cast(_Float16, static_cast<uint16_t>(r & 1 ? hw[r >> 1] >> 16 : hw[r >> 1])));
@@ -1192,12 +1120,11 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         for (int t = 0; t < NT && t < 2 * kKAhead; ++t) kf[t] = kfrag(t);
         if constexpr (kUseMask) {
 #pragma unroll
-            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t)
-                if (unit_of(t) == t) fetch(t, mw[t]);
+            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t) fetch(t, mw[t]);
         }
 #pragma unroll
         for (int t = 0; t < NT && t < 2; ++t)
-            S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? unit_of(t) : 0]));
+            S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
 #pragma unroll
         for (int pr = 0; pr < kPairs; ++pr) {
             __builtin_amdgcn_sched_barrier(0);
@@ -1216,7 +1143,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             if constexpr (kUseMask) {
 #pragma unroll
                 for (int t = t0 + 2 * kMaskAhead; t < t0 + 2 * kMaskAhead + 2; ++t)
-                    if (t < NT && unit_of(t) == t) fetch(t, mw[t]);
+                    if (t < NT) fetch(t, mw[t]);
             }
             X8 pb;
             if constexpr (kKAhead == 1) {
@@ -1225,7 +1152,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             }
 #pragma unroll
             for (int t = t0 + 2; t < t0 + 4; ++t)
-                if (t < NT) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? unit_of(t) : 0]));
+                if (t < NT) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
             if constexpr (kKAhead != 1) pb = probs(S[t0], S[has1 ? t0 + 1 : t0], has1);
             accumulate(pb, v0, v1, has1, o, lacc);
             asm volatile("" : "+v"(o));  // as in the exact pass below
@@ -1251,7 +1178,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             __builtin_amdgcn_sched_barrier(0);
-            if (unit_of(t) == t) fetch(t, w);
+            fetch(t, w);
             const f32x4 sc = Frag<T>::mma32(lds_load<X8>(ka + t * kKTile * sizeof(T)), qf, cinit(t, w));
             m0 = fmaxf(fmaxf(m0, sc[0]), sc[1]);
             m1 = fmaxf(fmaxf(m1, sc[2]), sc[3]);
@@ -1274,12 +1201,11 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             const bool has1 = t0 + 1 < NT;
             MaskWords w0, w1;
             fetch(t0, w0);
-            if (has1 && unit_of(t0 + 1) != t0) fetch(t0 + 1, w1);
-            const MaskWords& w1u = unit_of(t0 + 1) == t0 ? w0 : w1;
+            if (has1) fetch(t0 + 1, w1);
             const f32x4 s0 = Frag<T>::mma32(lds_load<X8>(kb + t0 * kKTile * sizeof(T)), qf, cinit(t0, w0) - m);
             f32x4 s1 = s0;
             if (has1)
-                s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), qf, cinit(t0 + 1, w1u) - m);
+                s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), qf, cinit(t0 + 1, w1) - m);
             const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
             const X4 v1 = has1 ? lds_read_tr<T>(vrow + kVTile * (t0 + 1)) : v0;
             accumulate(probs(s0, s1, has1), v0, v1, has1, o, lacc);
@@ -1513,8 +1439,6 @@ swin_attention_d16_kernel(const Params p) {
     constexpr int kQBufs = HPW > 1 ? 1 : 2;
     static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
     constexpr bool kRecs = HPW > 1;  // token-record K/V layout shared by the head slots
-    // paired key order (key_of) on the LDS-DMA path with a mask tensor
-    constexpr bool kPaired = kVec && v_row_major<T>() && mask_tensor(kMask);
     // (kRecs: K and V in one record array, k_lds; the last load's spill
     // lands in its padding)
     constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * 16;
@@ -1601,7 +1525,7 @@ swin_attention_d16_kernel(const Params p) {
     int rec_off[kRecs ? kRecRounds<St, kRecs>() : 1];
     if constexpr (kRecs) {
 #pragma unroll
-        for (int r = 0; r < kRecRounds<St, kRecs>(); ++r) rec_off[r] = St::template rec_voff<kPaired>(p, r);
+        for (int r = 0; r < kRecRounds<St, kRecs>(); ++r) rec_off[r] = St::rec_voff(p, r);
     }
     auto stage_load = [&](int bw, int sb) {
         if constexpr (kSpread) {
@@ -1609,7 +1533,7 @@ swin_attention_d16_kernel(const Params p) {
             const auto wd = St::template window_desc<kRecs>(p, bw, h, h0);
 #pragma unroll
             for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r)
-                St::template dma_round<kRecs, kPaired>(p, wd, k_lds[sb], vt_lds[sb], r, kRecs ? rec_off[r] : 0);
+                St::template dma_round<kRecs>(p, wd, k_lds[sb], vt_lds[sb], r, kRecs ? rec_off[r] : 0);
         } else {
             st.load(p, bw, h, q0, k_lds[sb], vt_lds[sb]);
         }
@@ -1630,7 +1554,7 @@ swin_attention_d16_kernel(const Params p) {
         // waiting for the bias loads after that request would wait for the
         // rows as well.
         if (active && (code != code_cur || rebuild)) {  // code is workgroup-uniform
-            build_tiles<NT, kMask, sizeof(T) == 2, kPaired>(bs, p, h, qi, g, code, cls_lds, off);
+            build_tiles<NT, kMask, sizeof(T) == 2>(bs, p, h, qi, g, code, cls_lds, off);
             code_cur = code;
             rebuild = false;
         }
@@ -1650,7 +1574,7 @@ swin_attention_d16_kernel(const Params p) {
         }
         const auto issue = [&]() {
             if constexpr (kSpread)
-                return DmaIssuer<T, St, kRecs, kPaired>{&p, St::template window_desc<kRecs>(p, b_next, h, h0),
+                return DmaIssuer<T, St, kRecs>{&p, St::template window_desc<kRecs>(p, b_next, h, h0),
                                                          k_lds[buf ^ 1], vt_lds[buf ^ 1], rec_off, i + 1 < i1};
             else
                 return NoIssue{};
@@ -1666,10 +1590,10 @@ swin_attention_d16_kernel(const Params p) {
             if constexpr (kTensor) use_mask = flag;
             if constexpr (sizeof(T) == 2) {
                 if (use_mask)
-                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, kPaired, Issuer>(
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, Issuer>(
                         p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
                 else
-                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, kPaired, Issuer>(
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, Issuer>(
                         p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
             } else {
                 if (use_mask)
