@@ -34,7 +34,7 @@ ARCH = "gfx950"
 
 HIP_SOURCES = [
     "api.hip", "partition.hip", "attn_mask.hip", "attention.hip",
-    "attention_f16.hip", "attention_bf16.hip", "attention_f32.hip", "attention_wide.hip",
+    "attention_f16.hip", "attention_bf16.hip", "attention_f32.hip", "attention_d32.hip", "attention_wide.hip",
     "window_linear.hip",
 ]
 

@@ -201,7 +201,14 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                       : mask_dtype == CRUMPET_DTYPE_F32  ? attn::kMaskF32
                       : mask_dtype == CRUMPET_DTYPE_BF16 ? attn::kMaskBF16
                                                          : attn::kMaskF16;
-    if (wide) {
+    // head dim 32 runs the tuned kernel for 2-byte types with vector IO at
+    // 14 or 22 tiles (129 <= N <= 352), addressed with 32-bit byte offsets
+    bool tuned32 = Dh == 32 && dtype != CRUMPET_DTYPE_F32 && vec && N <= 512 &&
+                   attn::d32_tiles(attn::select_tiles(N));
+    for (int i = 0; i < 3; ++i) {
+        if (((N - 1) * st[i][2] + 32) * esize >= (int64_t(1) << 31)) tuned32 = false;
+    }
+    if (wide && !tuned32) {
         attn::launch_wide(p, static_cast<int>(Dh), kmask, dtype, mask_dtype, s);
         return check_launch(what);
     }
@@ -219,7 +226,7 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                          k_strides[2] >= 0 &&
                          ((N - 1) * k_strides[2] + kv_bytes / esize + 16 * attn::kHeadsPerWg) * esize <
                              (int64_t(1) << 31);
-    p.hpw = (dtype != CRUMPET_DTYPE_F32 && p.vec_io && attn::multi_head_tiles(NT) &&
+    p.hpw = (!tuned32 && dtype != CRUMPET_DTYPE_F32 && p.vec_io && attn::multi_head_tiles(NT) &&
              (!attn::mask_tensor(kmask) || (boundary == nullptr && kmask != attn::kMaskF32)) &&
              Hh % attn::kHeadsPerWg == 0 && records)
                 ? attn::kHeadsPerWg
@@ -238,7 +245,9 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.launched = xcd_launch_count(p.chunks);
 
 
-    if (dtype == CRUMPET_DTYPE_F16)
+    if (tuned32)
+        attn::launch_d32(p, NT, kmask, dtype, s);
+    else if (dtype == CRUMPET_DTYPE_F16)
         attn::launch_f16(p, NT, kmask, s);
     else if (dtype == CRUMPET_DTYPE_BF16)
         attn::launch_bf16(p, NT, kmask, s);

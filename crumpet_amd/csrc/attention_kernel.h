@@ -174,6 +174,10 @@ struct Params {
 void launch_f16(const Params& p, int NT, int kmask, hipStream_t s);
 void launch_bf16(const Params& p, int NT, int kmask, hipStream_t s);
 void launch_f32(const Params& p, int NT, int kmask, hipStream_t s);
+// Head dim 32 on the tuned kernel (attention_d32.hip): 2-byte types, vector
+// IO, 14 or 22 tiles (d32_tiles), one head per workgroup.
+void launch_d32(const Params& p, int NT, int kmask, int32_t dtype, hipStream_t s);
+constexpr bool d32_tiles(int NT) { return NT == 14 || NT == 22; }
 
 // General kernel (attention_wide.hip): head dims 16, 32, 64 and 128, any N
 // (shifted-window regions up to kWideMaxRegionN tokens).  The caller has
@@ -318,12 +322,32 @@ __device__ __forceinline__ constexpr int kidx(int row, int d) {
         return row * 16 + d;
 }
 
-// Q layout in LDS: 2-byte types keep 32 elements per row, the rounded
-// q * scale * log2(e) (dims 0-15) and the rounding remainder (dims 16-31);
-// fp32 keeps the 16 dims of q * scale.
+// Head dim 32 (2-byte types): a Q row holds 64 elements, hi = q * scale
+// rounded (dims 0-31; scale includes log2(e)) and lo = the rounding
+// remainder (32-63), as store_q4 does for head dim 16; each score tile then
+// takes two 16x16x32 products over the same K fragment (Q_hi, then Q_lo),
+// since the head dim fills the product's depth.  A key tile stores dims
+// 8c .. 8c + 7 of its 16 rows as block c = 0..3 (16 B per row), so the lanes
+// of lane group g that read one key fragment (row col, dims 8g .. 8g + 7)
+// cover 256 contiguous bytes; V rows are plain (64 B).
 template <typename T>
-constexpr int q_row_elems() {
-    return sizeof(T) == 2 ? 32 : 16;
+__device__ __forceinline__ void store_q8(T* row, int d0, typename Frag<T>::x8 v, float scale) {
+    typename Frag<T>::x8 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = static_cast<float>(v[e]) * scale;
+        hi[e] = T(x);
+        lo[e] = T(x - static_cast<float>(hi[e]));
+    }
+    *reinterpret_cast<typename Frag<T>::x8*>(row + d0) = hi;
+    *reinterpret_cast<typename Frag<T>::x8*>(row + 32 + d0) = lo;
+}
+
+// Elements per Q row in LDS: 2-byte types keep q * scale as a hi/lo pair
+// (32 elements at head dim 16, 64 at head dim 32); fp32 keeps 16.
+template <typename T, int D>
+constexpr int q_row_len() {
+    return sizeof(T) == 2 ? 2 * D : 16;
 }
 
 template <typename T>
@@ -496,8 +520,9 @@ __device__ __forceinline__ V lds_load(uint32_t addr) {
 // Staging of one window's Q (this group's rows), K and V into LDS.  Each
 // thread owns chunks c = tid + k * kThreads of 4 elements; kQChunks Q chunks
 // come first, then NP*4 K chunks, then NP*4 V chunks.
-template <typename T, int NT, bool kVec>
+template <typename T, int NT, bool kVec, int D = 16>
 struct Stage {
+    static_assert(D == 16, "head dim 32 runs the LDS-DMA staging");
     static constexpr int NP = NT * 16;
     static constexpr int kQRows = 16 * kWaves;
     static constexpr int kQChunks = kQRows * 4;
@@ -538,7 +563,7 @@ struct Stage {
         for (int k = 0; k < kPerThread; ++k) {
             const int c = threadIdx.x + k * kThreads;
             if (c < kQChunks) {
-                store_q4<T>(&q_lds[(c >> 2) * q_row_elems<T>()], (c & 3) * 4, r[k], scale);
+                store_q4<T>(&q_lds[(c >> 2) * q_row_len<T, 16>()], (c & 3) * 4, r[k], scale);
             } else if (c < kChunks) {
                 const int cc = c - kQChunks;
                 if (cc < NP * 4) {
@@ -598,36 +623,53 @@ __device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, int voff) {
                  : "memory", "m0");
 }
 
-template <typename T, int NT>
-struct Stage<T, NT, true> {
+template <typename T, int D>
+struct QVec {
+    typedef typename Frag<T>::x4 type;
+};
+template <typename T>
+struct QVec<T, 32> {
+    typedef typename Frag<T>::x8 type;
+};
+
+template <typename T, int NT, int D>
+struct Stage<T, NT, true, D> {
+    static_assert(D == 16 || (D == 32 && sizeof(T) == 2), "head dim 32: 2-byte types");
     static constexpr int NP = NT * 16;
     static constexpr int kQRows = 16 * kWaves;
     static constexpr bool kDma = v_row_major<T>();
     static constexpr int kKC = (NP + 63) / 64;          // register path: rows per thread
     static constexpr int kRows = kDma ? (NP + 31) / 32 * 32 : kKC * 64;
-    static constexpr int kRounds = (kRows + 127) / 128;  // DMA path: 32-row loads per wave
+    // DMA path: per round a wave loads 32 K rows and 32 V rows (head dim
+    // 16), or 16 of each (head dim 32): 1 KB each
+    static constexpr int kRounds = D == 16 ? (kRows + 127) / 128 : (kRows + 63) / 64;
     static constexpr int kVtStride = kRows + 4;
-    static constexpr int kVLds = v_row_major<T>() ? kRows * 16 : 16 * kVtStride;
+    static constexpr int kVLds = v_row_major<T>() ? kRows * D : 16 * kVtStride;
     typedef typename Frag<T>::x4 X4;
+    // a thread's Q elements: 4 dims (head dim 16) or 8 (head dim 32)
+    typedef typename QVec<T, D>::type QV;
 
-    X4 rq, rk[kDma ? 1 : kKC], rv[kDma ? 1 : kKC];
+    QV rq;
+    X4 rk[kDma ? 1 : kKC], rv[kDma ? 1 : kKC];
 
-    static __device__ __forceinline__ X4 ld(__amdgpu_buffer_rsrc_t rs, int off) {
-        if constexpr (sizeof(X4) == 8)
-            return __builtin_bit_cast(X4, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+    template <typename V = X4>
+    static __device__ __forceinline__ V ld(__amdgpu_buffer_rsrc_t rs, int off) {
+        if constexpr (sizeof(V) == 8)
+            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
         else
-            return __builtin_bit_cast(X4, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
+            return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0));
     }
 
     static __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t off,
                                                                  int64_t s2, int N) {
         char* ub = uniform_ptr(static_cast<const char*>(base) + off * int64_t(sizeof(T)));
         const int extent = __builtin_amdgcn_readfirstlane(
-            static_cast<int>((int64_t(N - 1) * s2 + 16) * int64_t(sizeof(T))));
+            static_cast<int>((int64_t(N - 1) * s2 + D) * int64_t(sizeof(T))));
         return __builtin_amdgcn_make_buffer_rsrc(ub, 0, extent, 0x00020000);
     }
 
     __device__ __forceinline__ void load(const Params& p, int b, int h, int q0, T* k_dst, T* v_dst) {
+        static_assert(D == 16, "head dim 32 stages through load_q and the DMA rounds");
         const int N = p.N;
         const int tid = threadIdx.x & (kThreads - 1);  // within the head slot
         const int n0 = tid >> 2;
@@ -657,10 +699,10 @@ struct Stage<T, NT, true> {
     __device__ __forceinline__ void load_q(const Params& p, int b, int h, int q0) {
         const int N = p.N;
         const int tid = threadIdx.x & (kThreads - 1);
-        const int n0 = tid >> 2, d0 = (tid & 3) * 4;
+        const int n0 = tid >> 2, d0 = (tid & 3) * (D / 4);
         constexpr int es = sizeof(T);
         const auto qr = rsrc(p.q, int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1], p.qs[2], N);
-        rq = ld(qr, (min(q0 + n0, N - 1) * static_cast<int>(p.qs[2]) + d0) * es);
+        rq = ld<QV>(qr, (min(q0 + n0, N - 1) * static_cast<int>(p.qs[2]) + d0) * es);
     }
 
     // LDS-DMA rounds per wave for one window's K and V: kRounds with one
@@ -694,8 +736,8 @@ struct Stage<T, NT, true> {
     static __device__ __forceinline__ WindowDesc window_desc(const Params& p, int b, int h, int h0) {
         const int N = p.N;
         if constexpr (!kRecs) {
-            return {desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N),
-                    desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N)};
+            return {desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h) * p.ks[1], p.ks[2], N, D),
+                    desc_words<T>(p.v, int64_t(b) * p.vs[0] + int64_t(h) * p.vs[1], p.vs[2], N, D)};
         } else {
             const u32x4 d = desc_words<T>(p.k, int64_t(b) * p.ks[0] + int64_t(h0) * p.ks[1], p.ks[2], N,
                                           p.kv_delta + 16 * kHeadsPerWg);
@@ -725,7 +767,22 @@ struct Stage<T, NT, true> {
         const int lane = threadIdx.x & 63;
         typedef __attribute__((address_space(3))) T LdsT;
         const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
-        if constexpr (!kRecs) {
+        if constexpr (!kRecs && D == 32) {
+            // round r of wave w fills key tile 4r + w: K as 4 blocks of 8
+            // dims (lane l: block l/16, row l%16), V as 16 plain 64-byte rows
+            // (lane l: row l/4, dims 8*(l%4) ..)
+            (void)voff;
+            const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
+            const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
+            const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
+            const int row0 = 16 * (4 * r + wave);
+            if (row0 < kRows) {  // wave-uniform
+                const int nk = min(row0 + (lane & 15), N - 1);
+                dma16(wd.k, kl + row0 * 64, (nk * ks2 + 8 * (lane >> 4)) * es);
+                const int nv = min(row0 + (lane >> 2), N - 1);
+                dma16(wd.v, vl + row0 * 64, (nv * vs2 + 8 * (lane & 3)) * es);
+            }
+        } else if constexpr (!kRecs) {
             (void)voff;
             const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
             const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
@@ -750,9 +807,13 @@ struct Stage<T, NT, true> {
 
     __device__ __forceinline__ void store(float scale, T* q_lds, T* k_lds, T* vt_lds) const {
         const int tid = threadIdx.x & (kThreads - 1);  // within the head slot
-        const int n0 = tid >> 2, d0 = (tid & 3) * 4;
-        store_q4<T>(&q_lds[n0 * q_row_elems<T>()], d0, rq, scale);
+        const int n0 = tid >> 2;
+        if constexpr (D == 32)
+            store_q8<T>(&q_lds[n0 * 64], (tid & 3) * 8, rq, scale);
+        else
+            store_q4<T>(&q_lds[n0 * q_row_len<T, 16>()], (tid & 3) * 4, rq, scale);
         if constexpr (!kDma) {
+            const int d0 = (tid & 3) * 4;
 #pragma unroll
             for (int k = 0; k < kKC; ++k) {
                 *reinterpret_cast<X4*>(&k_lds[(tid + k * kThreads) * 4]) = rk[k];
@@ -976,7 +1037,7 @@ struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
 
-template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, typename Issue>
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, int D, typename Issue>
 __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
                                               const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
                                               int h, int wave, int qi, int col, int g, float& off,
@@ -987,19 +1048,34 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     constexpr int kPairs = (NT + 1) / 2;
     const int N = p.N;
 
+    static_assert(D == 16 || !kRec, "head dim 32: one head per workgroup");
     // Q^T operand of S^T = K Q^T (16x16x32): lane (col, g) holds elements
     // 8g..8g+7 of query col's LDS row, i.e. Q_hi dims for g < 2 and Q_lo
-    // dims for g >= 2.
-    const X8 qf = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * 32 + 8 * g]);
+    // dims for g >= 2 (head dim 16); head dim 32: Q_hi dims 8g..8g+7 (qf)
+    // and Q_lo dims 8g..8g+7 (qf_lo), two products per score tile.
+    const X8 qf = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * (2 * D) + 8 * g]);
+    X8 qf_lo = qf;
+    if constexpr (D == 32) qf_lo = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * 64 + 32 + 8 * g]);
+    // S^T of one tile from its K fragment and accumulator input
+    auto score = [&](const X8& kfr, const f32x4& c) -> f32x4 {
+        const f32x4 s = Frag<T>::mma32(kfr, qf, c);
+        if constexpr (D == 32)
+            return Frag<T>::mma32(kfr, qf_lo, s);
+        else
+            return s;
+    };
 
     // K operand: lane (col, g) reads row col of the tile, dims 8(g&1)..+7
-    // (kRec: k_lds and v_lds point at this head's row in the first record)
-    constexpr int kKTile = kRec ? 16 * kKRec : 256;  // elements from one K tile to the next
-    constexpr int kVTile = kRec ? 16 * kVRec : 256;
-    const T* kbase = kRec ? k_lds + col * kKRec + (g & 1) * 8 : k_lds + (g & 1) * 128 + col * 8;
+    // (head dim 16; kRec: k_lds and v_lds point at this head's row in the
+    // first record) or dims 8g..+7 (head dim 32)
+    constexpr int kKTile = kRec ? 16 * kKRec : 16 * D;  // elements from one K tile to the next
+    constexpr int kVTile = kRec ? 16 * kVRec : 16 * D;
+    const T* kbase = kRec ? k_lds + col * kKRec + (g & 1) * 8
+                          : k_lds + (D == 32 ? g : (g & 1)) * 128 + col * 8;
     auto kfrag = [&](int t) -> X8 { return *reinterpret_cast<const X8*>(kbase + t * kKTile); };
-    // V^T fragments by transpose reads of row-major V (lds_read_tr)
-    const T* vrow = &v_lds[(4 * g + (col >> 2)) * (kRec ? kVRec : 16) + (col & 3) * 4];
+    // V^T fragments by transpose reads of row-major V (lds_read_tr); head
+    // dim 32 reads dims 16..31 at vrow + 16 for the second half of O
+    const T* vrow = &v_lds[(4 * g + (col >> 2)) * (kRec ? kVRec : D) + (col & 3) * 4];
 
     // Tensor mask through a buffer descriptor spanning exactly the window's
     // [N, N] extent (see attend_f32 for the padding and end-of-extent rules).
@@ -1094,8 +1170,19 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         o = Frag<T>::mma32(va, pb, o);
         lacc = Frag<T>::mma32(ones8, pb, lacc);
     };
+    // head dim 32: O^T rows 16..31 += V^T (dims 16..31) P^T
+    auto accumulate_hi = [&](const X8& pb, const X4& v0, const X4& v1, bool has1, f32x4& o) {
+        X8 va;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            va[r] = v0[r];
+            va[r + 4] = has1 ? v1[r] : T(0.0f);
+        }
+        o = Frag<T>::mma32(va, pb, o);
+    };
 
     f32x4 o = {0.0f, 0.0f, 0.0f, 0.0f};
+    f32x4 o2 = {0.0f, 0.0f, 0.0f, 0.0f};  // head dim 32: dims 16..31
     f32x4 lacc = {0.0f, 0.0f, 0.0f, 0.0f};
     {
         // Software pipeline over tile pairs.  Iteration pr requests the V
@@ -1124,7 +1211,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         }
 #pragma unroll
         for (int t = 0; t < NT && t < 2; ++t)
-            S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
+            S[t] = score(kf[t], cinit(t, mw[kUseMask ? t : 0]));
 #pragma unroll
         for (int pr = 0; pr < kPairs; ++pr) {
             __builtin_amdgcn_sched_barrier(0);
@@ -1137,6 +1224,11 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             const bool has1 = t0 + 1 < NT;
             const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
             const X4 v1 = has1 ? lds_read_tr<T>(vrow + kVTile * (t0 + 1)) : v0;
+            X4 w0 = v0, w1 = v1;
+            if constexpr (D == 32) {
+                w0 = lds_read_tr<T>(vrow + 16 + kVTile * t0);
+                w1 = has1 ? lds_read_tr<T>(vrow + 16 + kVTile * (t0 + 1)) : w0;
+            }
 #pragma unroll
             for (int t = t0 + 2 * kKAhead; t < t0 + 2 * kKAhead + 2; ++t)
                 if (t < NT) kf[t] = kfrag(t);
@@ -1152,10 +1244,14 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             }
 #pragma unroll
             for (int t = t0 + 2; t < t0 + 4; ++t)
-                if (t < NT) S[t] = Frag<T>::mma32(kf[t], qf, cinit(t, mw[kUseMask ? t : 0]));
+                if (t < NT) S[t] = score(kf[t], cinit(t, mw[kUseMask ? t : 0]));
             if constexpr (kKAhead != 1) pb = probs(S[t0], S[has1 ? t0 + 1 : t0], has1);
             accumulate(pb, v0, v1, has1, o, lacc);
             asm volatile("" : "+v"(o));  // as in the exact pass below
+            if constexpr (D == 32) {
+                accumulate_hi(pb, w0, w1, has1, o2);
+                asm volatile("" : "+v"(o2));
+            }
         }
         __builtin_amdgcn_sched_barrier(0);
     }
@@ -1179,7 +1275,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         for (int t = 0; t < NT; ++t) {
             __builtin_amdgcn_sched_barrier(0);
             fetch(t, w);
-            const f32x4 sc = Frag<T>::mma32(lds_load<X8>(ka + t * kKTile * sizeof(T)), qf, cinit(t, w));
+            const f32x4 sc = score(lds_load<X8>(ka + t * kKTile * sizeof(T)), cinit(t, w));
             m0 = fmaxf(fmaxf(m0, sc[0]), sc[1]);
             m1 = fmaxf(fmaxf(m1, sc[2]), sc[3]);
             // keeps each tile's max here (pure math may otherwise be sunk
@@ -1189,6 +1285,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         __builtin_amdgcn_sched_barrier(0);
         const float m = xmax32(xmax16(fmaxf(m0, m1)));
         o = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        o2 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         lacc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         uint32_t kb = lds_byte_addr(kbase);
         int mvb = mvoff;
@@ -1202,16 +1299,23 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             MaskWords w0, w1;
             fetch(t0, w0);
             if (has1) fetch(t0 + 1, w1);
-            const f32x4 s0 = Frag<T>::mma32(lds_load<X8>(kb + t0 * kKTile * sizeof(T)), qf, cinit(t0, w0) - m);
+            const f32x4 s0 = score(lds_load<X8>(kb + t0 * kKTile * sizeof(T)), cinit(t0, w0) - m);
             f32x4 s1 = s0;
             if (has1)
-                s1 = Frag<T>::mma32(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), qf, cinit(t0 + 1, w1) - m);
+                s1 = score(lds_load<X8>(kb + (t0 + 1) * kKTile * sizeof(T)), cinit(t0 + 1, w1) - m);
             const X4 v0 = lds_read_tr<T>(vrow + kVTile * t0);
             const X4 v1 = has1 ? lds_read_tr<T>(vrow + kVTile * (t0 + 1)) : v0;
-            accumulate(probs(s0, s1, has1), v0, v1, has1, o, lacc);
+            const X8 pb = probs(s0, s1, has1);
+            accumulate(pb, v0, v1, has1, o, lacc);
             // keeps the O product in this iteration (it would otherwise be
             // sunk towards the store, keeping every V fragment live)
             asm volatile("" : "+v"(o));
+            if constexpr (D == 32) {
+                const X4 w0 = lds_read_tr<T>(vrow + 16 + kVTile * t0);
+                const X4 w1 = has1 ? lds_read_tr<T>(vrow + 16 + kVTile * (t0 + 1)) : w0;
+                accumulate_hi(pb, w0, w1, has1, o2);
+                asm volatile("" : "+v"(o2));
+            }
         }
         l = lacc[0];
         // move the offsets: a window like this one would have row sums
@@ -1221,7 +1325,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         exact = true;
     }
 
-    // lane holds O[qi][4g + r], r = 0..3
+    // lane holds O[qi][4g + r], r = 0..3 (head dim 32: and O[qi][16 + 4g + r])
     if (qi < N) {
         T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
         const float inv = 1.0f / l;
@@ -1230,7 +1334,14 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         for (int r = 0; r < 4; ++r) res[r] = T(o[r] * inv);
         if constexpr (kVec) {
             *reinterpret_cast<X4*>(orow + 4 * g) = res;
+            if constexpr (D == 32) {
+                X4 res2;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) res2[r] = T(o2[r] * inv);
+                *reinterpret_cast<X4*>(orow + 16 + 4 * g) = res2;
+            }
         } else {
+            static_assert(D == 16, "head dim 32 runs vector IO");
 #pragma unroll
             for (int r = 0; r < 4; ++r) orow[(4 * g + r) * p.os[3]] = res[r];
         }
@@ -1428,24 +1539,31 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
 // HPW heads per workgroup (1, or kHeadsPerWg on the LDS-DMA path): head slot
 // s = threadIdx.x / kThreads runs the kWaves strips of head h0 + s with its
 // own K/V buffers; the slots share the window walk and the barriers.
-template <typename T, int NT, int kMask, bool kVec, int HPW>
+// Head dim D = 32 (2-byte types, vector IO, one head): K and V take twice
+// the LDS, so they are single-buffered (3 workgroups per CU, which overlap
+// each other's staging): the next window's rows are requested after the
+// barrier that ends a window's compute.
+template <typename T, int NT, int kMask, bool kVec, int HPW, int D = 16>
 __global__ void __launch_bounds__(kThreads * HPW)
 __attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask, kVec>(), waves_per_eu<T, NT, kMask, kVec>())))
 swin_attention_d16_kernel(const Params p) {
-    typedef Stage<T, NT, kVec> St;
+    typedef Stage<T, NT, kVec, D> St;
     constexpr int NP = St::NP;
+    constexpr bool kSingle = D == 32;  // single-buffered K and V
+    static_assert(!kSingle || (HPW == 1 && kVec && v_row_major<T>()), "head dim 32: one head, LDS-DMA path");
     // Q rows are wave-private on the LDS-DMA path (a wave stores and reads
     // only its own 16 rows, in that order), so one buffer serves there.
-    constexpr int kQBufs = HPW > 1 ? 1 : 2;
+    constexpr int kQBufs = HPW > 1 || kSingle ? 1 : 2;
+    constexpr int kKVBufs = kSingle ? 1 : 2;
     static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
     constexpr bool kRecs = HPW > 1;  // token-record K/V layout shared by the head slots
     // (kRecs: K and V in one record array, k_lds; the last load's spill
     // lands in its padding)
-    constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * 16;
+    constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * D;
     constexpr int kVLdsAll = kRecs ? 8 : St::kVLds;
-    __shared__ __attribute__((aligned(16))) T q_lds[kQBufs][HPW][St::kQRows * q_row_elems<T>()];
-    __shared__ __attribute__((aligned(16))) T k_lds[2][kKLds];
-    __shared__ __attribute__((aligned(16))) T vt_lds[2][kVLdsAll];
+    __shared__ __attribute__((aligned(16))) T q_lds[kQBufs][HPW][St::kQRows * q_row_len<T, D>()];
+    __shared__ __attribute__((aligned(16))) T k_lds[kKVBufs][kKLds];
+    __shared__ __attribute__((aligned(16))) T vt_lds[kKVBufs][kVLdsAll];
     __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
     static_assert(sizeof(q_lds) + sizeof(k_lds) + sizeof(vt_lds) + sizeof(cls_lds) <= 160 * 1024,
                   "LDS footprint exceeds the 160 KB of a gfx950 CU");
@@ -1545,7 +1663,8 @@ swin_attention_d16_kernel(const Params p) {
 
     f32x4 bs[NT];
     for (int i = i0; i < i1; ++i) {
-        const int buf = (i - i0) & 1;
+        const int buf = kKVBufs == 2 ? (i - i0) & 1 : 0;
+        const int nbuf = kKVBufs == 2 ? buf ^ 1 : 0;  // the next window's K/V buffer
         const int b = b_next;
         const int code = code_next;
         const bool flag = flag_next;
@@ -1564,18 +1683,18 @@ swin_attention_d16_kernel(const Params p) {
             if constexpr (kMask != kNoMask && kMask != kMaskRegion)
                 flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
             if constexpr (kSpread) {
-                if (active)
+                if (active || kSingle)
                     st.load_q(p, b_next, h, q0);
                 else
-                    stage_load(b_next, buf ^ 1);
+                    stage_load(b_next, nbuf);
             } else {
-                stage_load(b_next, buf ^ 1);
+                stage_load(b_next, nbuf);
             }
         }
         const auto issue = [&]() {
-            if constexpr (kSpread)
+            if constexpr (kSpread && !kSingle)
                 return DmaIssuer<T, St, kRecs>{&p, St::template window_desc<kRecs>(p, b_next, h, h0),
-                                                         k_lds[buf ^ 1], vt_lds[buf ^ 1], rec_off, i + 1 < i1};
+                                               k_lds[nbuf], vt_lds[nbuf], rec_off, i + 1 < i1};
             else
                 return NoIssue{};
         }();
@@ -1590,10 +1709,10 @@ swin_attention_d16_kernel(const Params p) {
             if constexpr (kTensor) use_mask = flag;
             if constexpr (sizeof(T) == 2) {
                 if (use_mask)
-                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, Issuer>(
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, D, Issuer>(
                         p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
                 else
-                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, Issuer>(
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, D, Issuer>(
                         p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
             } else {
                 if (use_mask)
@@ -1602,8 +1721,16 @@ swin_attention_d16_kernel(const Params p) {
                     attend_f32<T, NT, kMask, false, kVec>(p, bs, qw, kw, vw, b, h, wave, qi, col, g);
             }
         }
-        if (i + 1 < i1)
-            st.store(qscale, q_lds[kQBufs == 2 ? buf ^ 1 : 0][slot], k_lds[buf ^ 1], vt_lds[buf ^ 1]);
+        if constexpr (kSingle) {
+            if (i + 1 < i1) {
+                __syncthreads();  // every wave is done with this window's K and V
+                const auto wd = St::template window_desc<false>(p, b_next, h, h0);
+#pragma unroll
+                for (int r = 0; r < St::template dma_rounds<false>(); ++r)
+                    St::template dma_round<false>(p, wd, k_lds[0], vt_lds[0], r, 0);
+            }
+        }
+        if (i + 1 < i1) st.store(qscale, q_lds[kQBufs == 2 ? buf ^ 1 : 0][slot], k_lds[nbuf], vt_lds[nbuf]);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // LDS-DMA rows have landed
         __syncthreads();
     }
@@ -1650,6 +1777,38 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
     }
 #undef CRUMPET_ATTN_NT
 #undef CRUMPET_ATTN_MASK
+}
+
+// Launch of the head-dim-32 kernel for element type T (2-byte).
+template <typename T>
+void launch32(const Params& p, int NT, int kmask, hipStream_t s) {
+    const dim3 grid(p.launched), block(kThreads);
+#define CRUMPET_ATTN32(NTV)                                                                                  \
+    case NTV:                                                                                               \
+        switch (kmask) {                                                                                    \
+            case kNoMask:                                                                                   \
+                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kNoMask, true, 1, 32>), grid, block, 0, s, p); \
+                break;                                                                                      \
+            case kMaskF16:                                                                                  \
+                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskF16, true, 1, 32>), grid, block, 0, s, p); \
+                break;                                                                                      \
+            case kMaskF32:                                                                                  \
+                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskF32, true, 1, 32>), grid, block, 0, s, p); \
+                break;                                                                                      \
+            case kMaskBF16:                                                                                 \
+                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskBF16, true, 1, 32>), grid, block, 0, s, p); \
+                break;                                                                                      \
+            default:                                                                                        \
+                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskRegion, true, 1, 32>), grid, block, 0, s, p); \
+                break;                                                                                      \
+        }                                                                                                   \
+        break;
+    switch (NT) {
+        CRUMPET_ATTN32(14)
+        CRUMPET_ATTN32(22)
+        default: break;
+    }
+#undef CRUMPET_ATTN32
 }
 
 }  // namespace
