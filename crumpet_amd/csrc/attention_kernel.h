@@ -1546,7 +1546,7 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
 template <typename T, int NT, int kMask, bool kVec, int HPW, int D = 16>
 __global__ void __launch_bounds__(kThreads * HPW)
 __attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask, kVec>(), waves_per_eu<T, NT, kMask, kVec>())))
-swin_attention_d16_kernel(const Params p) {
+swin_attention_tuned_kernel(const Params p) {
     typedef Stage<T, NT, kVec, D> St;
     constexpr int NP = St::NP;
     constexpr bool kSingle = D == 32;  // single-buffered K and V
@@ -1745,14 +1745,14 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
         if (p.vec_io) {                                                                               \
             if constexpr (v_row_major<T>() && multi_head_tiles(NTV) && MK != kMaskF32) {              \
                 if (p.hpw == kHeadsPerWg) {                                                           \
-                    hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true, kHeadsPerWg>), grid, \
+                    hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, MK, true, kHeadsPerWg>), grid, \
                                        block, 0, s, p);                                               \
                     break;                                                                            \
                 }                                                                                     \
             }                                                                                         \
-            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, true, 1>), grid, block, 0, s, p); \
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, MK, true, 1>), grid, block, 0, s, p); \
         } else {                                                                                      \
-            hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, MK, false, 1>), grid, block, 0, s, p); \
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, MK, false, 1>), grid, block, 0, s, p); \
         }                                                                                             \
     } while (0)
 #define CRUMPET_ATTN_NT(NTV)                                            \
@@ -1787,19 +1787,19 @@ void launch32(const Params& p, int NT, int kmask, hipStream_t s) {
     case NTV:                                                                                               \
         switch (kmask) {                                                                                    \
             case kNoMask:                                                                                   \
-                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kNoMask, true, 1, 32>), grid, block, 0, s, p); \
+                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kNoMask, true, 1, 32>), grid, block, 0, s, p); \
                 break;                                                                                      \
             case kMaskF16:                                                                                  \
-                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskF16, true, 1, 32>), grid, block, 0, s, p); \
+                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskF16, true, 1, 32>), grid, block, 0, s, p); \
                 break;                                                                                      \
             case kMaskF32:                                                                                  \
-                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskF32, true, 1, 32>), grid, block, 0, s, p); \
+                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskF32, true, 1, 32>), grid, block, 0, s, p); \
                 break;                                                                                      \
             case kMaskBF16:                                                                                 \
-                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskBF16, true, 1, 32>), grid, block, 0, s, p); \
+                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskBF16, true, 1, 32>), grid, block, 0, s, p); \
                 break;                                                                                      \
             default:                                                                                        \
-                hipLaunchKernelGGL((swin_attention_d16_kernel<T, NTV, kMaskRegion, true, 1, 32>), grid, block, 0, s, p); \
+                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskRegion, true, 1, 32>), grid, block, 0, s, p); \
                 break;                                                                                      \
         }                                                                                                   \
         break;

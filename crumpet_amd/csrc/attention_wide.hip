@@ -1,7 +1,7 @@
 // General fused window attention for the shapes the head-dim-16 kernel does
 // not cover: head dims 32, 64 and 128, and windows of more than 512 tokens
 // (any head dim of 16..128 that is a power of two, any N).  Same contract
-// and the same three mask modes as swin_attention_d16_kernel
+// and the same three mask modes as swin_attention_tuned_kernel
 // (attention_kernel.h); the numerics are the reference's:
 //
 //   S = (q * scale) k^T + bias[h] + mask,  out = softmax_rows(S) v
