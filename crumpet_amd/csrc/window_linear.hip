@@ -486,6 +486,15 @@ window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __r
     gemm_store<Tc, kKSteps>(L.a, L.o, L.rows, w, bias, y, ts, f_begin, f_end, pre);
 }
 
+// Orders a wave's LDS accesses to its own LDS slice across its lanes (the
+// streaming kernels below run their waves independently: no workgroup
+// barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // window_proj for 2-byte types with C and n_out at most 64 (stage 0 of Swin
 // UNETR: 48 and 48): the whole weight matrix fits in a wave's registers,
 // so waves run independently, without workgroup barriers.  A wave takes
@@ -495,22 +504,21 @@ window_proj_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __r
 // Fragment layout (v_mfma_f32_16x16x16, token = B column = lane & 15, lane
 // group q = lane >> 4): the contraction order is free as long as A and B
 // agree, so step kk, element j of lane group q contracts channel
-// 4*KS*q + 4*kk + j: lane group q holds the contiguous channels
-// [4*KS*q, 4*KS*(q+1)) of its token.  Likewise output row 4*q + i of
-// feature tile ft is feature 4*FT*q + 4*ft + i, so the lane's FT result
-// quads are the contiguous features [4*FT*q, 4*FT*(q+1)) of its token.
-//
-// Memory side: kLdsIn / kLdsOut move a tile's rows between memory and the
-// wave's LDS slice as 16-byte vectors, lane i on vector i of the tile
-// (whole rows, adjacent lanes on adjacent bytes), and the fragments between
-// LDS and registers; otherwise each lane loads / stores its own 8-byte
-// pieces of its token's row.
+// 4*KS*q + 4*kk + j: lane group q loads the contiguous channels
+// [4*KS*q, 4*KS*(q+1)) of its token's window row as KS 8-byte pieces.
+// Likewise output row 4*q + i of feature tile ft is feature
+// 4*FT*q + 4*ft + i, so the lane's FT result quads are the contiguous
+// features [4*FT*q, 4*FT*(q+1)) of its token; they go to the wave's LDS
+// slice, and the tile's 16 consecutive output rows leave as 16-byte
+// non-temporal vectors (per-lane 8-byte non-temporal stores were 2.4x
+// slower: partial-line non-temporal writes; staging the input rows through
+// LDS as well measured no faster).
 //
 // Tile assignment: at step s, logical wave L takes tile s * waves + L, with
 // L numbered so that the waves of one XCD (workgroups x, x + 8, ... under
 // round-robin dispatch) hold a contiguous run of tiles; the window-buffer
 // lines that straddle two neighbouring tiles are then fetched into one L2.
-template <typename Tc, int KS, int FT, int kDepth, bool kLdsIn, bool kLdsOut>
+template <typename Tc, int KS, int FT, int kDepth>
 __global__ void __launch_bounds__(kThreads)
 window_proj_stream_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __restrict__ w,
                           const Tc* __restrict__ bias, const WinGeom g, uint32_t tiles) {
@@ -519,12 +527,9 @@ window_proj_stream_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const 
     typedef uint32_t V16 __attribute__((ext_vector_type(4)));
     constexpr int C = 16 * KS, NO = 16 * FT;
     constexpr int kWavesPerWg = kThreads / 64;
-    constexpr int kPad = 8;                              // elements: rows 16 bytes apart in bank order
-    constexpr int kInVecs = 16 * C / 8;                  // 16-byte vectors of a tile's input rows
-    constexpr int kInIters = kLdsIn ? (kInVecs + 63) / 64 : KS;
+    constexpr int kPad = 8;  // elements: rows 16 bytes apart in bank order
     constexpr int kOutVecs = 16 * NO / 8;
-    __shared__ __attribute__((aligned(16))) Tc in_lds[kLdsIn ? kWavesPerWg : 1][kLdsIn ? 16 * (C + kPad) : 8];
-    __shared__ __attribute__((aligned(16))) Tc out_lds[kLdsOut ? kWavesPerWg : 1][kLdsOut ? 16 * (NO + kPad) : 8];
+    __shared__ __attribute__((aligned(16))) Tc out_lds[kWavesPerWg][16 * (NO + kPad)];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int col = lane & 15;
@@ -544,61 +549,20 @@ window_proj_stream_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const 
         b4[ft] = bias ? load4(bias + 4 * FT * q + 4 * ft) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // raw rows of one tile in registers: 16-byte vectors (kLdsIn) or the
-    // lane's 8-byte fragments
-    struct Raw {
-        V16 v[kLdsIn ? kInIters : 1];
-        X4 f[kLdsIn ? 1 : KS];
+    // the lane's fragments of tile t (tiles clamped to the last, so that the
+    // loads are unconditional; tokens past the volume read row 0 and are not
+    // stored)
+    auto load_tile = [&](uint32_t t, X4(&xf)[KS]) {
+        const uint32_t v = min(t, tiles - 1) * 16 + col;
+        const uint32_t row = v < g.vtokens ? window_token(v, g) : 0u;
+        const Tc* src = win + int64_t(row) * C + 4 * KS * q;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) xf[kk] = *reinterpret_cast<const X4*>(src + 4 * kk);
     };
-    // rows of tile t (clamped to the last tile, so that the loads are
-    // unconditional; tokens past the volume read row 0 and are not stored)
-    auto load_tile = [&](uint32_t t, Raw& r) {
-        const uint32_t t16 = min(t, tiles - 1) * 16;
-        if constexpr (kLdsIn) {
-#pragma unroll
-            for (int it = 0; it < kInIters; ++it) {
-                const int i = min(lane + 64 * it, kInVecs - 1);
-                const int tok = i / (C / 8);
-                const uint32_t v = t16 + tok;
-                const uint32_t row = v < g.vtokens ? window_token(v, g) : 0u;
-                r.v[it] = *reinterpret_cast<const V16*>(win + int64_t(row) * C + 8 * (i - tok * (C / 8)));
-            }
-        } else {
-            const uint32_t v = t16 + col;
-            const uint32_t row = v < g.vtokens ? window_token(v, g) : 0u;
-            const Tc* src = win + int64_t(row) * C + 4 * KS * q;
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) r.f[kk] = *reinterpret_cast<const X4*>(src + 4 * kk);
-        }
-    };
-    auto wave_sync = []() {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
-    auto run_tile = [&](uint32_t t, const Raw& r) {
-        X4 xf[KS];
-        if constexpr (kLdsIn) {
-            Tc* il = in_lds[wave];
-            wave_sync();  // the previous tile's fragment reads are done
-#pragma unroll
-            for (int it = 0; it < kInIters; ++it) {
-                const int i = lane + 64 * it;
-                const int tok = i / (C / 8);
-                if (i < kInVecs)
-                    *reinterpret_cast<V16*>(&il[tok * (C + kPad) + 8 * (i - tok * (C / 8))]) = r.v[it];
-            }
-            wave_sync();
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk)
-                xf[kk] = *reinterpret_cast<const X4*>(&il[col * (C + kPad) + 4 * KS * q + 4 * kk]);
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) xf[kk] = r.f[kk];
-        }
+    auto run_tile = [&](uint32_t t, const X4(&xf)[KS]) {
         const uint32_t t16 = t * 16;
         Tc* ol = out_lds[wave];
-        if constexpr (kLdsOut) wave_sync();
+        wave_lds_sync();  // the previous tile's vectors have been read
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
             f32x4 acc = b4[ft];
@@ -607,37 +571,30 @@ window_proj_stream_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const 
             T4 o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = static_cast<Tc>(acc[e]);
-            if constexpr (kLdsOut) {
-                *reinterpret_cast<T4*>(&ol[col * (NO + kPad) + 4 * FT * q + 4 * ft]) = o;
-            } else {
-                const uint32_t v = t16 + col;
-                if (v < g.vtokens) *reinterpret_cast<T4*>(y + int64_t(v) * NO + 4 * FT * q + 4 * ft) = o;
-            }
+            *reinterpret_cast<T4*>(&ol[col * (NO + kPad) + 4 * FT * q + 4 * ft]) = o;
         }
-        if constexpr (kLdsOut) {
-            wave_sync();
+        wave_lds_sync();
 #pragma unroll
-            for (int it = 0; it < (kOutVecs + 63) / 64; ++it) {
-                const int i = lane + 64 * it;
-                const int tok = i / (NO / 8);
-                const int part = i - tok * (NO / 8);
-                if (i < kOutVecs && t16 + tok < g.vtokens)
-                    __builtin_nontemporal_store(*reinterpret_cast<const V16*>(&ol[tok * (NO + kPad) + 8 * part]),
-                                                reinterpret_cast<V16*>(y + int64_t(t16 + tok) * NO + 8 * part));
-            }
+        for (int it = 0; it < (kOutVecs + 63) / 64; ++it) {
+            const int i = lane + 64 * it;
+            const int tok = i / (NO / 8);
+            const int part = i - tok * (NO / 8);
+            if (i < kOutVecs && t16 + tok < g.vtokens)
+                __builtin_nontemporal_store(*reinterpret_cast<const V16*>(&ol[tok * (NO + kPad) + 8 * part]),
+                                            reinterpret_cast<V16*>(y + int64_t(t16 + tok) * NO + 8 * part));
         }
     };
 
-    Raw raw[kDepth];
+    X4 xb[kDepth][KS];
 #pragma unroll
-    for (int d = 0; d < kDepth; ++d) load_tile(L + d * waves, raw[d]);
+    for (int d = 0; d < kDepth; ++d) load_tile(L + d * waves, xb[d]);
     for (uint32_t t0 = L; t0 < tiles; t0 += kDepth * waves) {
 #pragma unroll
         for (int d = 0; d < kDepth; ++d) {
             const uint32_t t = t0 + d * waves;
             if (t < tiles) {  // wave-uniform
-                run_tile(t, raw[d]);
-                load_tile(t + kDepth * waves, raw[d]);
+                run_tile(t, xb[d]);
+                load_tile(t + kDepth * waves, xb[d]);
             }
         }
     }
@@ -714,11 +671,6 @@ window_qkv_stream_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const v
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) r.v[kk] = *reinterpret_cast<const Tx4*>(src + 4 * kk);
     };
-    auto wave_sync = []() {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    };
     auto run_tile = [&](uint32_t t, const Raw& r) {
         f32x4 v[KS];
 #pragma unroll
@@ -758,7 +710,7 @@ window_qkv_stream_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const v
 #pragma unroll
             for (int e = 0; e < 4; ++e) xf[kk][e] = static_cast<Tc>(v[kk][e]);
         Tc* ol = out_lds[wave];
-        wave_sync();  // the previous tile's vectors have been read
+        wave_lds_sync();  // the previous tile's vectors have been read
 #pragma unroll
         for (int ft = 0; ft < FT; ++ft) {
             f32x4 acc = *reinterpret_cast<const f32x4*>(b_lds + 4 * ft);
@@ -769,7 +721,7 @@ window_qkv_stream_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const v
             for (int e = 0; e < 4; ++e) o[e] = static_cast<Tc>(acc[e]);
             *reinterpret_cast<T4*>(&ol[col * (NO + kPad) + 4 * FT * q + 4 * ft]) = o;
         }
-        wave_sync();
+        wave_lds_sync();
         const uint32_t t16 = t * 16;
 #pragma unroll
         for (int it = 0; it < (kOutVecs + 63) / 64; ++it) {
@@ -944,7 +896,6 @@ void launch_proj(dim3 grid, size_t lds, hipStream_t s, void* y, const void* win,
 
 // The register-resident projection: 2-byte types, C and n_out at most 64.
 constexpr int kStreamDepth = 2;               // tiles in flight per wave
-constexpr bool kStreamLdsIn = false, kStreamLdsOut = true;
 constexpr uint32_t kStreamWorkgroups = 768;  // 3 per CU, 12 waves per CU
 
 bool proj_streams(int32_t dtype, int64_t C, int64_t n_out) {
@@ -1001,7 +952,7 @@ template <typename Tc, int KS>
 void launch_proj_stream_ks(int FT, dim3 grid, hipStream_t s, void* y, const void* win, const void* w,
                            const void* bias, const WinGeom& g, uint32_t tiles) {
 #define CRUMPET_PROJ_STREAM(F)                                                                        \
-    hipLaunchKernelGGL((window_proj_stream_kernel<Tc, KS, F, kStreamDepth, kStreamLdsIn, kStreamLdsOut>), grid, dim3(kThreads), 0, s, \
+    hipLaunchKernelGGL((window_proj_stream_kernel<Tc, KS, F, kStreamDepth>), grid, dim3(kThreads), 0, s, \
                        static_cast<Tc*>(y), static_cast<const Tc*>(win), static_cast<const Tc*>(w),   \
                        static_cast<const Tc*>(bias), g, tiles)
     switch (FT) {
