@@ -12,9 +12,11 @@
 //   The relative-position bias is the same for every window, so it is kept in
 //   registers instead of being re-read per window: a workgroup owns one head
 //   (4 waves) or kHeadsPerWg heads (12 waves) and a group of 4 consecutive
-//   16-query strips of each, and walks a range of windows (contiguous; every
-//   ranges-th window with a mask tensor and boundary flags, whose flagged
-//   windows cost more and come in runs).  Each wave builds the fp32 bias
+//   16-query strips of each, and walks a range of windows (contiguous; with
+//   a mask tensor every ranges-th window of a mask-major order, because
+//   windows whose boundary flag is set cost more and come in runs, and the
+//   windows that read one mask then run together on one XCD).  Each wave
+//   builds the fp32 bias
 //   tiles of its strip (NT tiles of 16 keys x 16 queries, 4 values per lane
 //   each) once, straight from the caller's bias tensor (any float dtype and
 //   strides), and uses them as the accumulator input of every window's
@@ -48,7 +50,7 @@
 //   input type in place and fed straight into v_mfma_f32_16x16x32_{f16,bf16}
 //   (two key tiles per instruction); the row sums ride on the same pipe as
 //   ones^T P^T.  O^T lands as 4 consecutive head-dim values of one query per
-//   lane, which is one 8-byte store.
+//   lane, which is one 8-byte store (two at head dim 32).
 //
 // Softmax (2-byte types, attend_offset)
 //   Scores are produced in log2 units (Q carries scale * log2(e) as a hi/lo
@@ -59,6 +61,14 @@
 //   is as good as with the exact max; a strip that misses it is redone with
 //   the exact max, and its offsets move for the next window.  fp32
 //   (attend_f32) keeps an online softmax over key chunks.
+//
+// Head dim 32 (D = 32; 2-byte types, vector IO, 14 or 22 tiles, one head per
+//   workgroup)
+//   The head dim fills the 32-deep score product, so Q_hi and Q_lo take one
+//   product each per score tile over the same K fragment; V^T enters in two
+//   16-dim halves with two output accumulators.  K and V take twice the LDS,
+//   so they are single-buffered and three workgroups per CU overlap each
+//   other's staging.
 //
 // Padding
 //   Keys are padded to NP = 16*NT: padded key columns get a -inf bias
