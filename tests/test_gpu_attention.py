@@ -214,6 +214,35 @@ def test_non_unit_d_stride(oracle, dev):
     _compare(out, ref, dtype, "non-unit d stride")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+def test_rows_8_byte_aligned(oracle, dev, dtype, masked):
+    """q, k, v and out with a row stride of 20 elements (unit d stride, rows
+    8-byte but not 16-byte aligned), without a mask (multi-head token
+    records) and with a per-window mask under boundary flags: the 16-byte
+    K/V transfers and Q loads then start at 8-byte-aligned offsets."""
+    B, H, N = 6, 3, 343
+    bufs = [seeded((B, H, N, 20), dtype, 820 + i) for i in range(3)]
+    q, k, v = (t[..., :16] for t in bufs)
+    bias = _bias(H, N, dtype, 823)
+    mask = bnd = None
+    if masked:
+        mask = torch.where(seeded((2, N, N), torch.float32, 824) > 0.7, -100.0, 0.0).to(dtype)
+        bnd = torch.tensor([1, 0, 1, 1, 0, 1], dtype=torch.uint8)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None if mask is None else _f32(mask),
+                           None if bnd is None else bnd.numpy(), scale=0.25)
+    # slice on the device: .to() of a non-dense view would make it contiguous
+    qd, kd, vd = (t.to(dev)[..., :16] for t in bufs)
+    out_buf = torch.full((B, H, N, 20), float("nan"), dtype=dtype, device=dev)
+    out = out_buf[..., :16]
+    for t in (qd, kd, vd, out):
+        assert t.stride(2) == 20 and t.stride(3) == 1 and t.data_ptr() % 16 == 0
+    fused_swin_attention_windows(qd, kd, vd, bias.to(dev), None if mask is None else mask.to(dev),
+                                 None if bnd is None else bnd.to(dev), 0.25, out)
+    _compare(out, ref, dtype, f"8-byte-aligned rows {dtype} masked={masked}")
+    assert torch.isnan(out_buf[..., 16:].float()).all()  # nothing written past the head dim
+
+
 def test_config3_stage0_all_windows(oracle, dev):
     """qkv [1372, 343, 144] fp16, table [2197, 3] trunc-normal 0.02,
     49^3 shifted mask tiled over sw-batch 4, scale 0.25.  Every window against

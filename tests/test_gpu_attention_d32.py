@@ -138,3 +138,24 @@ def test_config3_shape_sampled(oracle, dev, dtype):
     for name, out in (("region", out_r), ("tensor", out_t)):
         assert torch.isfinite(out.float()).all()
         _compare(out[torch.from_numpy(idx).to(dev)], ref, dtype, f"config-3 shape d32 {name} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", DT, ids=IDS)
+def test_rows_8_byte_aligned(oracle, dev, dtype):
+    """q, k, v and out with a row stride of 36 elements (unit d stride, rows
+    8-byte but not 16-byte aligned): the 16-byte Q loads and K/V transfers
+    then start at 8-byte-aligned offsets."""
+    B, H, N = 5, 2, 300
+    bufs = [seeded((B, H, N, 36), dtype, 5400 + i) for i in range(3)]
+    q, k, v = (t[..., :32] for t in bufs)
+    bias = seeded((H, N, N), torch.float32, 5403) * 0.5
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=0.25)
+    # slice on the device: .to() of a non-dense view would make it contiguous
+    qd, kd, vd = (t.to(dev)[..., :32] for t in bufs)
+    out_buf = torch.full((B, H, N, 36), float("nan"), dtype=dtype, device=dev)
+    out = out_buf[..., :32]
+    for t in (qd, kd, vd, out):
+        assert t.stride(2) == 36 and t.stride(3) == 1 and t.data_ptr() % 16 == 0
+    fused_swin_attention_windows(qd, kd, vd, bias.to(dev), None, None, 0.25, out)
+    _compare(out, ref, dtype, f"d32 8-byte-aligned rows {dtype}")
+    assert torch.isnan(out_buf[..., 32:].float()).all()  # nothing written past the head dim
