@@ -623,14 +623,17 @@ __device__ __forceinline__ u32x4 desc_words(const void* base, int64_t off, int64
 // lds_addr + 16 * lane (lds_addr wave-uniform).  Written as inline asm so
 // that the compiler does not treat it as an LDS store it must wait for
 // before unrelated LDS reads; the caller waits (vmcnt(0)) before the barrier
-// that publishes the rows.  gfx950 needs one wait state between an SALU
-// write of M0 and an LDS-DMA load that reads it; the compiler's hazard
-// recognizer does not look inside inline asm, hence the explicit s_nop.
+// that publishes the rows.  The LDS address enters as an operand bound to
+// M0, so the compiler writes M0 itself and knows it is live (a clobber of
+// the reserved M0 would not be honoured).  gfx950 needs one wait state
+// between an SALU write of M0 and an LDS-DMA load that reads it; the
+// compiler's hazard recognizer does not look inside inline asm, hence the
+// s_nop ahead of the load.
 __device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, int voff) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
-                 : "s"(lds_addr), "v"(voff), "s"(desc)
-                 : "memory", "m0");
+                 : "v"(voff), "s"(desc), "{m0}"(lds_addr)
+                 : "memory");
 }
 
 template <typename T, int D>
