@@ -232,7 +232,22 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                 ? attn::kHeadsPerWg
                 : 1;
     p.kv_delta = p.hpw > 1 ? static_cast<int32_t>(kv_bytes / esize) : 0;
-    const int64_t units = Hh / p.hpw * p.groups;
+    // head dim 32 at 21 or 22 strips (321 <= N <= 352: the 7^3 windows):
+    // kHeadsPerWg strip groups of one head per workgroup, sharing
+    // double-buffered K and V (3 of 24 waves idle at most, as in the 4-wave
+    // form; fewer strips would idle more of them).  fp32 masks need 2 waves
+    // per SIMD, too few for the 12-wave workgroup.  With boundary flags the
+    // 4-wave form stays: its three workgroups per CU mix flagged and clear
+    // windows, where the strip groups would all wait on a flagged window's
+    // mask together.
+    const bool group_slots = tuned32 && attn::d32_group_slots(NT, p.strips) && kmask != attn::kMaskF32 &&
+                             (!attn::mask_tensor(kmask) || boundary == nullptr);
+    if (group_slots) {
+        p.hpw = attn::kHeadsPerWg;
+        p.kv_delta = 0;
+        p.groups = (p.groups + attn::kHeadsPerWg - 1) / attn::kHeadsPerWg;  // blocks of strip groups
+    }
+    const int64_t units = (group_slots ? Hh : Hh / p.hpw) * p.groups;
     const int64_t target = p.hpw > 1 ? kTargetWorkgroupsMultiHead : kTargetWorkgroups;
     int64_t wpw = (B * units + target - 1) / target;
     if (wpw < 1) wpw = 1;

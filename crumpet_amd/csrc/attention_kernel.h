@@ -185,9 +185,15 @@ void launch_f16(const Params& p, int NT, int kmask, hipStream_t s);
 void launch_bf16(const Params& p, int NT, int kmask, hipStream_t s);
 void launch_f32(const Params& p, int NT, int kmask, hipStream_t s);
 // Head dim 32 on the tuned kernel (attention_d32.hip): 2-byte types, vector
-// IO, 14 or 22 tiles (d32_tiles), one head per workgroup.
+// IO, 14 or 22 tiles (d32_tiles), one head per workgroup: 4 waves
+// (p.hpw = 1), or kHeadsPerWg strip groups of 4 waves (p.hpw = kHeadsPerWg)
+// at 22 tiles when the strips leave at most 3 of the 24 waves of a head's
+// two workgroups idle, as many as the 4-wave form does (d32_group_slots).
 void launch_d32(const Params& p, int NT, int kmask, int32_t dtype, hipStream_t s);
 constexpr bool d32_tiles(int NT) { return NT == 14 || NT == 22; }
+constexpr bool d32_group_slots(int NT, int strips) {
+    return NT == 22 && strips % (kWaves * kHeadsPerWg) >= kWaves * kHeadsPerWg - 3;
+}
 
 // General kernel (attention_wide.hip): head dims 16, 32, 64 and 128, any N
 // (shifted-window regions up to kWideMaxRegionN tokens).  The caller has
@@ -720,10 +726,14 @@ struct Stage<T, NT, true, D> {
 
     // LDS-DMA rounds per wave for one window's K and V: kRounds with one
     // head per workgroup, one record load per round with kHeadsPerWg heads.
-    template <bool kRecs>
+    // Head dim 32: kStageWaves waves share a window's key tiles (kWaves, or
+    // all the waves of a workgroup of several strip groups).
+    template <bool kRecs, int kStageWaves = kWaves>
     static constexpr int dma_rounds() {
         constexpr int kAllWaves = kWaves * kHeadsPerWg;
-        return kRecs ? (rec_loads(NT) + kAllWaves - 1) / kAllWaves : kRounds;
+        if constexpr (kRecs) return (rec_loads(NT) + kAllWaves - 1) / kAllWaves;
+        if constexpr (D == 32) return (kRows / 16 + kStageWaves - 1) / kStageWaves;
+        return kRounds;
     }
 
     // Round r of this wave's LDS-DMA loads of window b's K and V.  16 bytes
@@ -771,24 +781,27 @@ struct Stage<T, NT, true, D> {
         return (min(n, N - 1) * static_cast<int>(p.ks[2]) + part) * static_cast<int>(sizeof(T));
     }
 
-    template <bool kRecs>
+    template <bool kRecs, int kStageWaves = kWaves>
     static __device__ __forceinline__ void dma_round(const Params& p, const WindowDesc& wd, T* k_dst, T* v_dst,
                                                      int r, int voff) {
         static_assert(kDma, "LDS-DMA staging");
+        static_assert(kStageWaves == kWaves || D == 32, "shared staging: head dim 32");
         const int N = p.N;
         constexpr int es = sizeof(T);
         const int lane = threadIdx.x & 63;
         typedef __attribute__((address_space(3))) T LdsT;
         const uint32_t kl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)k_dst));
         if constexpr (!kRecs && D == 32) {
-            // round r of wave w fills key tile 4r + w: K as 4 blocks of 8
-            // dims (lane l: block l/16, row l%16), V as 16 plain 64-byte rows
+            // round r of wave w (of the kStageWaves waves of the workgroup)
+            // fills key tile kStageWaves * r + w: K as 4 blocks of 8 dims
+            // (lane l: block l/16, row l%16), V as 16 plain 64-byte rows
             // (lane l: row l/4, dims 8*(l%4) ..)
             (void)voff;
             const uint32_t vl = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((LdsT*)v_dst));
             const int ks2 = static_cast<int>(p.ks[2]), vs2 = static_cast<int>(p.vs[2]);
-            const int wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & (kWaves - 1));
-            const int row0 = 16 * (4 * r + wave);
+            const int wave = __builtin_amdgcn_readfirstlane(
+                kStageWaves == kWaves ? (threadIdx.x >> 6) & (kWaves - 1) : static_cast<int>(threadIdx.x >> 6));
+            const int row0 = 16 * (kStageWaves * r + wave);
             if (row0 < kRows) {  // wave-uniform
                 const int nk = min(row0 + (lane & 15), N - 1);
                 dma16(wd.k, kl + row0 * 64, (nk * ks2 + 8 * (lane >> 4)) * es);
@@ -1032,9 +1045,9 @@ constexpr int kRecRounds() {
 // attend_offset spreads them over its tile pairs, so that a workgroup's
 // loads reach the memory pipeline a few at a time while it computes instead
 // of all at the window start (where every wave would stall on issue).
-template <typename T, typename St, bool kRecs>
+template <typename T, typename St, bool kRecs, int kStageWaves = kWaves>
 struct DmaIssuer {
-    static constexpr int kRounds = St::template dma_rounds<kRecs>();
+    static constexpr int kRounds = St::template dma_rounds<kRecs, kStageWaves>();
     const Params* p;
     typename St::WindowDesc wd;  // the next window's descriptors
     T* k_dst;
@@ -1042,7 +1055,7 @@ struct DmaIssuer {
     const int* voff;  // records: the lane's offset per round
     bool on;          // a next window exists (wave-uniform)
     __device__ __forceinline__ void operator()(int r) const {
-        if (on) St::template dma_round<kRecs>(*p, wd, k_dst, v_dst, r, kRecs ? voff[r] : 0);
+        if (on) St::template dma_round<kRecs, kStageWaves>(*p, wd, k_dst, v_dst, r, kRecs ? voff[r] : 0);
     }
 };
 struct NoIssue {
@@ -1553,23 +1566,29 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
 // s = threadIdx.x / kThreads runs the kWaves strips of head h0 + s with its
 // own K/V buffers; the slots share the window walk and the barriers.
 // Head dim D = 32 (2-byte types, vector IO, one head): K and V take twice
-// the LDS, so they are single-buffered (3 workgroups per CU, which overlap
-// each other's staging): the next window's rows are requested after the
-// barrier that ends a window's compute.
+// the LDS.  With HPW = 1 they are single-buffered (3 workgroups per CU,
+// which overlap each other's staging): the next window's rows are requested
+// after the barrier that ends a window's compute.  With HPW > 1 the slots
+// are HPW strip groups of one head (12 waves, one workgroup per CU) that
+// share double-buffered K and V, staged by all the waves during the compute.
 template <typename T, int NT, int kMask, bool kVec, int HPW, int D = 16>
 __global__ void __launch_bounds__(kThreads * HPW)
 __attribute__((amdgpu_waves_per_eu(waves_per_eu<T, NT, kMask, kVec>(), waves_per_eu<T, NT, kMask, kVec>())))
 swin_attention_tuned_kernel(const Params p) {
     typedef Stage<T, NT, kVec, D> St;
     constexpr int NP = St::NP;
-    constexpr bool kSingle = D == 32;  // single-buffered K and V
-    static_assert(!kSingle || (HPW == 1 && kVec && v_row_major<T>()), "head dim 32: one head, LDS-DMA path");
+    constexpr bool kGroupSlots = D == 32 && HPW > 1;  // the slots are strip groups of one head
+    constexpr bool kSingle = D == 32 && HPW == 1;     // single-buffered K and V
+    static_assert(D == 16 || (kVec && v_row_major<T>()), "head dim 32: LDS-DMA path");
+    constexpr int kStageWaves = kGroupSlots ? kWaves * HPW : kWaves;  // waves sharing a window's DMA
+    static_assert(!kGroupSlots || waves_per_eu<T, NT, kMask, kVec>() * 4 >= kWaves * HPW,
+                  "the strip groups' waves must fit one CU's SIMDs together");
     // Q rows are wave-private on the LDS-DMA path (a wave stores and reads
     // only its own 16 rows, in that order), so one buffer serves there.
     constexpr int kQBufs = HPW > 1 || kSingle ? 1 : 2;
     constexpr int kKVBufs = kSingle ? 1 : 2;
     static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
-    constexpr bool kRecs = HPW > 1;  // token-record K/V layout shared by the head slots
+    constexpr bool kRecs = HPW > 1 && !kGroupSlots;  // token-record K/V layout shared by the head slots
     // (kRecs: K and V in one record array, k_lds; the last load's spill
     // lands in its padding)
     constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * D;
@@ -1583,15 +1602,18 @@ swin_attention_tuned_kernel(const Params p) {
 
     uint32_t chunk;
     if (!xcd_chunk(blockIdx.x, p.launched, p.chunks, chunk)) return;
-    // chunk = (range * (H / HPW) + head block) * groups + group: the groups of
-    // one (range, head block) are consecutive, hence on one XCD, and share
-    // its L2 for K/V.
+    // chunk = (range * head blocks + head block) * groups + group: the groups
+    // of one (range, head block) are consecutive, hence on one XCD, and
+    // share its L2 for K/V.  A head block is HPW heads, or one head whose
+    // strip groups HPW * group .. + HPW - 1 are the slots (kGroupSlots;
+    // p.groups then counts blocks of HPW strip groups).
     const int slot = HPW > 1 ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) / kThreads) : 0;
-    const int hb_count = p.H / HPW;
-    const int grp = static_cast<int>(chunk % p.groups);
+    constexpr int kHeads = kGroupSlots ? 1 : HPW;  // heads per workgroup
+    const int hb_count = p.H / kHeads;
+    const int grp = kGroupSlots ? static_cast<int>(chunk % p.groups) * HPW + slot : static_cast<int>(chunk % p.groups);
     const int rh = static_cast<int>(chunk / p.groups);
-    const int h0 = (rh % hb_count) * HPW;  // first head of the workgroup
-    const int h = h0 + slot;
+    const int h0 = (rh % hb_count) * kHeads;  // first head of the workgroup
+    const int h = kGroupSlots ? h0 : h0 + slot;
     const int range = rh / hb_count;
     // Tensor-mask modes take every ranges-th window (range, range + ranges,
     // ...): a window whose boundary flag is set costs more than one whose
@@ -1663,8 +1685,9 @@ swin_attention_tuned_kernel(const Params p) {
             st.load_q(p, bw, h, q0);
             const auto wd = St::template window_desc<kRecs>(p, bw, h, h0);
 #pragma unroll
-            for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r)
-                St::template dma_round<kRecs>(p, wd, k_lds[sb], vt_lds[sb], r, kRecs ? rec_off[r] : 0);
+            for (int r = 0; r < St::template dma_rounds<kRecs, kStageWaves>(); ++r)
+                St::template dma_round<kRecs, kStageWaves>(p, wd, k_lds[sb], vt_lds[sb], r,
+                                                           kRecs ? rec_off[r] : 0);
         } else {
             st.load(p, bw, h, q0, k_lds[sb], vt_lds[sb]);
         }
@@ -1706,8 +1729,8 @@ swin_attention_tuned_kernel(const Params p) {
         }
         const auto issue = [&]() {
             if constexpr (kSpread && !kSingle)
-                return DmaIssuer<T, St, kRecs>{&p, St::template window_desc<kRecs>(p, b_next, h, h0),
-                                               k_lds[nbuf], vt_lds[nbuf], rec_off, i + 1 < i1};
+                return DmaIssuer<T, St, kRecs, kStageWaves>{&p, St::template window_desc<kRecs>(p, b_next, h, h0),
+                                                            k_lds[nbuf], vt_lds[nbuf], rec_off, i + 1 < i1};
             else
                 return NoIssue{};
         }();
@@ -1792,36 +1815,45 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
 #undef CRUMPET_ATTN_MASK
 }
 
-// Launch of the head-dim-32 kernel for element type T (2-byte).
+// Launch of the head-dim-32 kernel for element type T (2-byte) at NT tiles
+// with HPW slots: one head of 4 waves (HPW = 1) or kHeadsPerWg strip groups
+// of one head (no fp32 mask, d32_group_slots).
+template <typename T, int NT, int HPW>
+void launch32_slots(const Params& p, int kmask, hipStream_t s) {
+    const dim3 grid(p.launched), block(kThreads * HPW);
+    switch (kmask) {
+        case kNoMask:
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kNoMask, true, HPW, 32>), grid, block, 0, s, p);
+            break;
+        case kMaskF16:
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskF16, true, HPW, 32>), grid, block, 0, s, p);
+            break;
+        case kMaskF32:
+            if constexpr (HPW == 1)
+                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskF32, true, 1, 32>), grid, block, 0, s, p);
+            break;
+        case kMaskBF16:
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskBF16, true, HPW, 32>), grid, block, 0, s, p);
+            break;
+        default:
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskRegion, true, HPW, 32>), grid, block, 0, s,
+                               p);
+            break;
+    }
+}
+
+// Launch of the head-dim-32 kernel for element type T (2-byte): p.hpw
+// selects the slots (set by the host together with p.groups).
 template <typename T>
 void launch32(const Params& p, int NT, int kmask, hipStream_t s) {
-    const dim3 grid(p.launched), block(kThreads);
-#define CRUMPET_ATTN32(NTV)                                                                                  \
-    case NTV:                                                                                               \
-        switch (kmask) {                                                                                    \
-            case kNoMask:                                                                                   \
-                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kNoMask, true, 1, 32>), grid, block, 0, s, p); \
-                break;                                                                                      \
-            case kMaskF16:                                                                                  \
-                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskF16, true, 1, 32>), grid, block, 0, s, p); \
-                break;                                                                                      \
-            case kMaskF32:                                                                                  \
-                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskF32, true, 1, 32>), grid, block, 0, s, p); \
-                break;                                                                                      \
-            case kMaskBF16:                                                                                 \
-                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskBF16, true, 1, 32>), grid, block, 0, s, p); \
-                break;                                                                                      \
-            default:                                                                                        \
-                hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, kMaskRegion, true, 1, 32>), grid, block, 0, s, p); \
-                break;                                                                                      \
-        }                                                                                                   \
-        break;
-    switch (NT) {
-        CRUMPET_ATTN32(14)
-        CRUMPET_ATTN32(22)
-        default: break;
+    if (NT == 14) {
+        launch32_slots<T, 14, 1>(p, kmask, s);
+    } else if (NT == 22) {
+        if (p.hpw == kHeadsPerWg && kmask != kMaskF32)
+            launch32_slots<T, 22, kHeadsPerWg>(p, kmask, s);
+        else
+            launch32_slots<T, 22, 1>(p, kmask, s);
     }
-#undef CRUMPET_ATTN32
 }
 
 }  // namespace

@@ -46,21 +46,25 @@ def _qkv_views(B, N, H, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", DT, ids=IDS)
-@pytest.mark.parametrize("N", [129, 200, 224, 225, 343, 352])
-@pytest.mark.parametrize("mode", ["none", "mask_f16", "mask_bf16", "mask_f32"])
+@pytest.mark.parametrize("N", [129, 200, 224, 225, 320, 321, 343, 352])
+@pytest.mark.parametrize("mode", ["none", "mask_f16", "mask_bf16", "mask_f32", "mask_f16_noflags"])
 def test_tile_edges_and_mask_kinds(oracle, dev, N, dtype, mode):
-    """Both tile classes at their edges (14 tiles: 129..224, 22: 225..352),
-    without a mask and with a per-window mask of each dtype read as
-    mask[b mod 3] under boundary flags, fp32 bias with -inf-free values."""
+    """Both tile classes at their edges (14 tiles: 129..224, 22: 225..352;
+    at 22 tiles, 21 and 22 strips (N >= 321) run three strip groups per
+    workgroup without a mask or without boundary flags, N = 320 the 4-wave
+    form), without a mask and with a per-window mask of each dtype read as
+    mask[b mod 3] under boundary flags (fp16 also without flags), fp32 bias
+    with -inf-free values."""
     B, H = 12, 2
     q, k, v = (seeded((B, H, N, 32), dtype, 5000 + N + i) for i in range(3))
     bias = seeded((H, N, N), torch.float32, 5010 + N) * 0.5
     mask = bnd = None
     if mode != "none":
-        mdt = {"mask_f16": torch.float16, "mask_bf16": torch.bfloat16, "mask_f32": torch.float32}[mode]
+        mdt = {"mask_bf16": torch.bfloat16, "mask_f32": torch.float32}.get(mode, torch.float16)
         m = torch.where(seeded((3, N, N), torch.float32, 5020 + N) > 0.8, -100.0, 0.0)
         mask = (m + seeded((3, N, N), torch.float32, 5030 + N) * 0.25).to(mdt)
-        bnd = torch.tensor([1, 0, 1, 1, 0, 1, 0, 0, 1, 1, 1, 0], dtype=torch.uint8)
+        if mode != "mask_f16_noflags":
+            bnd = torch.tensor([1, 0, 1, 1, 0, 1, 0, 0, 1, 1, 1, 0], dtype=torch.uint8)
     print(f"d32 N={N} {dtype} {mode}", flush=True)
     ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None if mask is None else _f32(mask),
                            None if bnd is None else bnd.numpy(), scale=0.25)
@@ -141,11 +145,13 @@ def test_config3_shape_sampled(oracle, dev, dtype):
 
 
 @pytest.mark.parametrize("dtype", DT, ids=IDS)
-def test_rows_8_byte_aligned(oracle, dev, dtype):
+@pytest.mark.parametrize("N", [300, 343])
+def test_rows_8_byte_aligned(oracle, dev, dtype, N):
     """q, k, v and out with a row stride of 36 elements (unit d stride, rows
-    8-byte but not 16-byte aligned): the 16-byte Q loads and K/V transfers
-    then start at 8-byte-aligned offsets."""
-    B, H, N = 5, 2, 300
+    8-byte but not 16-byte aligned), in the 4-wave form (N = 300) and with
+    three strip groups per workgroup (N = 343): the 16-byte Q loads and K/V
+    transfers then start at 8-byte-aligned offsets."""
+    B, H = 5, 2
     bufs = [seeded((B, H, N, 36), dtype, 5400 + i) for i in range(3)]
     q, k, v = (t[..., :32] for t in bufs)
     bias = seeded((H, N, N), torch.float32, 5403) * 0.5
@@ -157,5 +163,5 @@ def test_rows_8_byte_aligned(oracle, dev, dtype):
     for t in (qd, kd, vd, out):
         assert t.stride(2) == 36 and t.stride(3) == 1 and t.data_ptr() % 16 == 0
     fused_swin_attention_windows(qd, kd, vd, bias.to(dev), None, None, 0.25, out)
-    _compare(out, ref, dtype, f"d32 8-byte-aligned rows {dtype}")
+    _compare(out, ref, dtype, f"d32 8-byte-aligned rows N={N} {dtype}")
     assert torch.isnan(out_buf[..., 32:].float()).all()  # nothing written past the head dim
