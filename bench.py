@@ -730,7 +730,8 @@ def profile_run(dev):
           lambda i: fused_swin_attention_shifted(views[i % 3][0], views[i % 3][1], views[i % 3][2], bias, vol,
                                                  (7, 7, 7), (3, 3, 3), 0.25, ov))
     del qkvs, views, o, ov, mask
-    # the general kernel: head dim 32 at the same window shape, shifted mode
+    # head dim 32 at the same window shape, shifted mode (the tuned kernel's
+    # strip-group form)
     qkvs = [seeded((Bw, N, 3 * Hh * 32), torch.float16, 320 + r).to(dev) for r in range(2)]
     views = [q.reshape(Bw, N, 3, Hh, 32).permute(2, 0, 3, 1, 4) for q in qkvs]
     o = torch.empty((Bw, N, Hh * 32), dtype=torch.float16, device=dev)
@@ -849,8 +850,10 @@ def main():
     if aw:
         flops = 2 * C3_FLOPS  # head dim 32
         comp_w = {"workload": "head dim 32 (feature size 96) at the config-3 window shape: 1372 windows x "
-                              "3 heads, N=343, fp16; the tuned kernel at head dim 32 (K/V single-buffered, "
-                              "Q as a hi/lo pair over two products per score tile)",
+                              "3 heads, N=343, fp16; the tuned kernel at head dim 32 (Q as a hi/lo pair "
+                              "over two products per score tile; shifted: three strip groups of one head "
+                              "per workgroup sharing double-buffered K/V; mask tensor with boundary flags: "
+                              "4-wave workgroups, K/V single-buffered)",
                   "flops": flops, "max_abs_err_vs_fp32": aw["max_abs_err"]}
         for key, t in (("shifted", aw["t_shift"]), ("tensor_mask", aw["t_tensor"])):
             tfl = flops / (t * 1e-3) / 1e12
