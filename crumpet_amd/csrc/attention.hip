@@ -9,6 +9,8 @@
 
 #include <math.h>
 
+#include <algorithm>
+
 #include "attention_kernel.h"
 #include "crumpet_common.h"
 #include "crumpet_hip.h"
@@ -21,7 +23,8 @@ namespace {
 // vector-IO kernels run 3 waves per SIMD); a partial last round costs more
 // than the extra prologues of smaller ranges.
 constexpr int64_t kTargetWorkgroups = 1536;
-// kHeadsPerWg workgroups take one CU's LDS each: one per CU
+// Workgroups of kHeadsPerWg slots (heads, or head-dim-32 strip groups)
+// take most of a CU's LDS: one per CU, 256 CUs
 constexpr int64_t kTargetWorkgroupsMultiHead = 256;
 
 int dtype_size(int32_t dt) {
@@ -248,8 +251,16 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         p.groups = (p.groups + attn::kHeadsPerWg - 1) / attn::kHeadsPerWg;  // blocks of strip groups
     }
     const int64_t units = (group_slots ? Hh : Hh / p.hpw) * p.groups;
-    const int64_t target = p.hpw > 1 ? kTargetWorkgroupsMultiHead : kTargetWorkgroups;
-    int64_t wpw = (B * units + target - 1) / target;
+    int64_t wpw;
+    if (p.hpw > 1) {
+        // one workgroup per CU: at most kTargetWorkgroupsMultiHead chunks, so
+        // that none waits for a second round behind full ranges (ranges of
+        // ceil(B * units / 256) windows gave 264 chunks at stages 1 and 2)
+        const int64_t max_ranges = std::max<int64_t>(1, kTargetWorkgroupsMultiHead / units);
+        wpw = (B + max_ranges - 1) / max_ranges;
+    } else {
+        wpw = (B * units + kTargetWorkgroups - 1) / kTargetWorkgroups;
+    }
     if (wpw < 1) wpw = 1;
     p.win_per_wg = static_cast<int32_t>(wpw);
     p.ranges = static_cast<int32_t>((B + wpw - 1) / wpw);

@@ -444,3 +444,39 @@ def test_last_key_of_last_row_16bit(oracle, dev, N, dt16):
     out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), None, scale=0.25)
     _compare(out, ref, dtype, f"N={N} {dt16} last key")
     _compare(out[:, :, N - 1], ref[:, :, N - 1], dtype, f"N={N} {dt16} last row")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("Dh", [16, 32])
+@pytest.mark.parametrize("masked", [False, True], ids=["nomask", "mask"])
+def test_row_sums_out_of_range_take_the_exact_pass(oracle, dev, dtype, Dh, masked):
+    """Windows whose row sums leave the offset softmax's range, between
+    ordinary ones: a head whose bias sits 20 below (natural units) the
+    others, so its first window's row sums are near 2^-20, and windows with
+    q = 3k, whose dominant diagonal reaches 2^40 and more (fp16 P overflow).
+    Each forces the exact pass and moves the offsets for the following
+    windows; B = 96 gives every workgroup several windows (multi-head records
+    and head-dim-32 strip groups without a mask, 4-wave workgroups with a
+    mask tensor and boundary flags).  The results must match the fp32 oracle
+    like any other window."""
+    B, H, N = 96, 3, 343
+    qkv = seeded((B, N, 3, H, Dh), dtype, 1300 + Dh)  # the MONAI layout: heads adjacent
+    peaky = [4, 5, 30, 31, 32, 61, 90]
+    qkv[peaky, :, 0] = (qkv[peaky, :, 1].float() * 3).to(dtype)
+    # a dominant diagonal makes a row's output its own v (up to ~5 for N(0, 1)
+    # values, where bf16 rounding alone exceeds 1e-2): v at a quarter scale
+    qkv[:, :, 2] = (qkv[:, :, 2].float() * 0.25).to(dtype)
+    q, k, v = qkv.permute(2, 0, 3, 1, 4)
+    bias = seeded((H, N, N), torch.float32, 1310) * 0.5
+    bias[1] -= 20.0
+    mask = bnd = None
+    if masked:
+        mask = torch.where(seeded((3, N, N), torch.float32, 1320) > 0.8, -100.0, 0.0).to(dtype)
+        bnd = (torch.arange(B) % 3 != 1).to(torch.uint8)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None if mask is None else _f32(mask),
+                           None if bnd is None else bnd.numpy(), scale=0.25)
+    qd, kd, vd = qkv.to(dev).permute(2, 0, 3, 1, 4)
+    out = fused_swin_attention_windows(qd, kd, vd, bias.to(dev), None if mask is None else mask.to(dev),
+                                       None if bnd is None else bnd.to(dev), 0.25,
+                                       torch.empty((B, H, N, Dh), dtype=dtype, device=dev))
+    _compare(out, ref, dtype, f"exact pass Dh={Dh} {dtype} masked={masked}")
