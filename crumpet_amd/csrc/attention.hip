@@ -251,16 +251,13 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
         p.groups = (p.groups + attn::kHeadsPerWg - 1) / attn::kHeadsPerWg;  // blocks of strip groups
     }
     const int64_t units = (group_slots ? Hh : Hh / p.hpw) * p.groups;
-    int64_t wpw;
-    if (p.hpw > 1) {
-        // one workgroup per CU: at most kTargetWorkgroupsMultiHead chunks, so
-        // that none waits for a second round behind full ranges (ranges of
-        // ceil(B * units / 256) windows gave 264 chunks at stages 1 and 2)
-        const int64_t max_ranges = std::max<int64_t>(1, kTargetWorkgroupsMultiHead / units);
-        wpw = (B + max_ranges - 1) / max_ranges;
-    } else {
-        wpw = (B * units + kTargetWorkgroups - 1) / kTargetWorkgroups;
-    }
+    // At most `target` chunks (whole rounds of resident workgroups), so that
+    // none waits for an extra round behind full ranges: ranges of
+    // ceil(B * units / target) windows gave 264 chunks for 256 CUs at stages
+    // 1 and 2.
+    const int64_t target = p.hpw > 1 ? kTargetWorkgroupsMultiHead : kTargetWorkgroups;
+    const int64_t max_ranges = std::max<int64_t>(1, target / units);
+    int64_t wpw = (B + max_ranges - 1) / max_ranges;
     if (wpw < 1) wpw = 1;
     p.win_per_wg = static_cast<int32_t>(wpw);
     p.ranges = static_cast<int32_t>((B + wpw - 1) / wpw);
