@@ -1017,27 +1017,31 @@ __device__ __forceinline__ float xmax32(float m) {
 // keep P inside the range where rounding to the input type costs no more
 // than with the exact max: every P finite (in fp16 a P either rounds to at
 // most 65504 or overflows to inf, and the row sum is the fp32 sum of the
-// rounded P, so a finite row sum means finite P) and a row sum of at least
-// kRowSumMin = 2^-3 (with at most 512 keys the largest P is then at least
-// 2^-12, a normal fp16 number, and a P that is subnormal carries less than
-// 2^-21 of the row's weight in rounding error).  The row sums come out of
-// the same pass (ones^T P^T), so the check is exact: when a strip's row sums
-// miss [2^-3, FLT_MAX] (a bad first guess, or scores that moved from earlier
-// windows), the wave redoes the strip with the exact row max subtracted in
-// the fp32 accumulator, as the reference does, and moves its offsets so that
-// a window like this one would have row sums near 2^kOffsetTarget; the
-// caller rebuilds the wave's bias tiles with them before its next window
-// (the tiles stay read-only here, which keeps them in registers).  The range
-// spans about 2^-3 .. 2^16 for the largest P, 9-10 octaves either side of
-// the target, so a window whose scores jump from its predecessors' (a
-// dominant diagonal, say) rarely costs the exact pass.
+// rounded P, so a finite row sum means finite P), a row sum of at most
+// kRowSumMax = 2^64 (bf16 P can be finite far above that; the bound keeps
+// the fp32 numerator P V finite for |v| below 2^64, and an fp16 row sum
+// never reaches it) and of at least kRowSumMin = 2^-3 (with at most 512
+// keys the largest P is then at least 2^-12, a normal fp16 number, and a P
+// that is subnormal carries less than 2^-21 of the row's weight in rounding
+// error).  The row sums come out of the same pass (ones^T P^T), so the check
+// is exact: when a strip's row sums miss [2^-3, 2^64] (a bad first guess,
+// or scores that moved from earlier windows), the wave redoes the strip
+// with the exact row max subtracted in the fp32 accumulator, as the
+// reference does, and moves its offsets so that a window like this one
+// would have row sums near 2^kOffsetTarget; the caller rebuilds the wave's
+// bias tiles with them before its next window (the tiles stay read-only
+// here, which keeps them in registers).  In fp16 the range spans about
+// 2^-3 .. 2^16 for the largest P, 9-10 octaves either side of the target,
+// so a window whose scores jump from its predecessors' (a dominant
+// diagonal, say) rarely costs the exact pass.
 //
 // Per score this leaves one exp and half a conversion on the VALU; with no
 // max reduction between the score tiles, pair p+1's score MFMAs are issued
 // next to pair p's exps, and K, V and mask fragments are requested one or
 // two pairs ahead.
 constexpr float kOffsetTarget = 7.0f;  // log2 of the row sum aimed at
-constexpr float kRowSumMin = 0.125f;   // row sums below this take the exact pass
+constexpr float kRowSumMin = 0.125f;   // row sums outside [kRowSumMin, kRowSumMax] take
+constexpr float kRowSumMax = 0x1p64f;  // the exact pass (NaN too)
 
 // LDS-DMA rounds per wave with token records (1 otherwise: an array size).
 template <typename St, bool kRecs>
@@ -1290,7 +1294,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     }
 
     float l = lacc[0];  // every row of ones^T P^T holds the sum of query col
-    const bool bad = qi < N && !(l >= kRowSumMin && l <= __FLT_MAX__);  // also NaN and inf
+    const bool bad = qi < N && !(l >= kRowSumMin && l <= kRowSumMax);  // also NaN and inf
     bool exact = false;  // the exact pass ran and moved the offsets (wave-uniform)
     if (__builtin_amdgcn_ballot_w64(bad) != 0) {
         // Exact pass: the row max of the scores, then the strip again with

@@ -452,8 +452,9 @@ def test_last_key_of_last_row_16bit(oracle, dev, N, dt16):
 def test_row_sums_out_of_range_take_the_exact_pass(oracle, dev, dtype, Dh, masked):
     """Windows whose row sums leave the offset softmax's range, between
     ordinary ones: a head whose bias sits 20 below (natural units) the
-    others, so its first window's row sums are near 2^-20, and windows with
-    q = 3k, whose dominant diagonal reaches 2^40 and more (fp16 P overflow).
+    others, so its first window's row sums are near 2^-20, windows with
+    q = 3k, whose dominant diagonal reaches 2^40 and more (fp16 P overflow),
+    and windows with q = 12k (row sums past 2^64 with finite bf16 P).
     Each forces the exact pass and moves the offsets for the following
     windows; B = 96 gives every workgroup several windows (multi-head records
     and head-dim-32 strip groups without a mask, 4-wave workgroups with a
@@ -463,6 +464,8 @@ def test_row_sums_out_of_range_take_the_exact_pass(oracle, dev, dtype, Dh, maske
     qkv = seeded((B, N, 3, H, Dh), dtype, 1300 + Dh)  # the MONAI layout: heads adjacent
     peaky = [4, 5, 30, 31, 32, 61, 90]
     qkv[peaky, :, 0] = (qkv[peaky, :, 1].float() * 3).to(dtype)
+    sharper = [50, 51, 75]  # row sums near 2^70: finite bf16 P past the 2^64 bound
+    qkv[sharper, :, 0] = (qkv[sharper, :, 1].float() * 12).to(dtype)
     # a dominant diagonal makes a row's output its own v (up to ~5 for N(0, 1)
     # values, where bf16 rounding alone exceeds 1e-2): v at a quarter scale
     qkv[:, :, 2] = (qkv[:, :, 2].float() * 0.25).to(dtype)
