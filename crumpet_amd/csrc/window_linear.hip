@@ -518,8 +518,11 @@ __device__ __forceinline__ void wave_lds_sync() {
 // L numbered so that the waves of one XCD (workgroups x, x + 8, ... under
 // round-robin dispatch) hold a contiguous run of tiles; the window-buffer
 // lines that straddle two neighbouring tiles are then fetched into one L2.
+// The grid (stream_grid, kStreamWorkgroups) keeps 3 workgroups per CU
+// resident, so the kernel asks for 3 waves per SIMD: 96 -> 96 fits that in
+// 165 VGPRs, where the compiler's own choice (171 with AGPRs) gave 2.
 template <typename Tc, int KS, int FT, int kDepth>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3)))
 window_proj_stream_kernel(Tc* __restrict__ y, const Tc* __restrict__ win, const Tc* __restrict__ w,
                           const Tc* __restrict__ bias, const WinGeom g, uint32_t tiles) {
     typedef typename Mma<Tc>::x4 X4;
@@ -898,8 +901,10 @@ void launch_proj(dim3 grid, size_t lds, hipStream_t s, void* y, const void* win,
 constexpr int kStreamDepth = 2;               // tiles in flight per wave
 constexpr uint32_t kStreamWorkgroups = 768;  // 3 per CU, 12 waves per CU
 
+// C and n_out up to 64, and 96 -> 96 (stage 1 of Swin UNETR at feature size
+// 48: 72 weight VGPRs per lane, still 3 waves per SIMD)
 bool proj_streams(int32_t dtype, int64_t C, int64_t n_out) {
-    return elem_size(dtype) == 2 && C <= 64 && n_out <= 64;
+    return elem_size(dtype) == 2 && ((C <= 64 && n_out <= 64) || (C == 96 && n_out == 96));
 }
 
 constexpr int kQkvStreamDepth = 1;
@@ -955,11 +960,16 @@ void launch_proj_stream_ks(int FT, dim3 grid, hipStream_t s, void* y, const void
     hipLaunchKernelGGL((window_proj_stream_kernel<Tc, KS, F, kStreamDepth>), grid, dim3(kThreads), 0, s, \
                        static_cast<Tc*>(y), static_cast<const Tc*>(win), static_cast<const Tc*>(w),   \
                        static_cast<const Tc*>(bias), g, tiles)
-    switch (FT) {
-        case 1: CRUMPET_PROJ_STREAM(1); break;
-        case 2: CRUMPET_PROJ_STREAM(2); break;
-        case 3: CRUMPET_PROJ_STREAM(3); break;
-        default: CRUMPET_PROJ_STREAM(4); break;
+    if constexpr (KS == 6) {
+        (void)FT;  // 96 -> 96 only (proj_streams)
+        CRUMPET_PROJ_STREAM(6);
+    } else {
+        switch (FT) {
+            case 1: CRUMPET_PROJ_STREAM(1); break;
+            case 2: CRUMPET_PROJ_STREAM(2); break;
+            case 3: CRUMPET_PROJ_STREAM(3); break;
+            default: CRUMPET_PROJ_STREAM(4); break;
+        }
     }
 #undef CRUMPET_PROJ_STREAM
 }
@@ -973,7 +983,8 @@ void launch_proj_stream(int KS, int FT, hipStream_t s, void* y, const void* win,
         case 1: launch_proj_stream_ks<Tc, 1>(FT, grid, s, y, win, w, bias, g, tiles); break;
         case 2: launch_proj_stream_ks<Tc, 2>(FT, grid, s, y, win, w, bias, g, tiles); break;
         case 3: launch_proj_stream_ks<Tc, 3>(FT, grid, s, y, win, w, bias, g, tiles); break;
-        default: launch_proj_stream_ks<Tc, 4>(FT, grid, s, y, win, w, bias, g, tiles); break;
+        case 4: launch_proj_stream_ks<Tc, 4>(FT, grid, s, y, win, w, bias, g, tiles); break;
+        default: launch_proj_stream_ks<Tc, 6>(FT, grid, s, y, win, w, bias, g, tiles); break;
     }
 }
 

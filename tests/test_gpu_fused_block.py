@@ -166,13 +166,13 @@ def test_window_qkv_stage0_full_size(oracle, dev, cdt):
 
 
 @pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
-@pytest.mark.parametrize("C,n_out", [(16, 16), (32, 48), (48, 48), (64, 64), (48, 16), (16, 64)])
+@pytest.mark.parametrize("C,n_out", [(16, 16), (32, 48), (48, 48), (64, 64), (48, 16), (16, 64), (96, 96)])
 @pytest.mark.parametrize("dims", [(1, 9, 10, 11), (3, 9, 9, 9), (1, 2, 3, 3)], ids=["990tok", "2187tok", "18tok"])
 def test_window_proj_register_path(oracle, dev, dims, C, n_out, cdt):
-    """2-byte types with C and n_out at most 64 take the register-resident
-    kernel (weights in registers, permuted contraction and feature order,
-    16-token tiles): token counts that leave a partial last tile, fewer
-    tiles than waves, and n_out != C."""
+    """2-byte types with C and n_out at most 64, and 96 -> 96 (stage 1), take
+    the register-resident kernel (weights in registers, permuted contraction
+    and feature order, 16-token tiles): token counts that leave a partial
+    last tile, fewer tiles than waves, and n_out != C."""
     B, D, H, W = dims
     ws, ss = (7, 7, 7), (3, 3, 3)
     Dp, Hp, Wp = (-(-n // k) * k for n, k in zip((D, H, W), ws))
