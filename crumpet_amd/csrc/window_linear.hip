@@ -752,6 +752,171 @@ window_qkv_stream_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const v
     }
 }
 
+// window_qkv for 2-byte compute types at C = 96 (stage 1 of Swin UNETR at
+// feature size 48: 96 -> 288).  The 55 KB weight matrix does not fit a
+// wave's registers, so it sits in LDS for the whole launch in fragment
+// order: fragment (c, ft, kk) is 64 lanes x 4 elements, contiguous, so each
+// A-operand read is one conflict-free 8-byte LDS load per lane.  Twelve
+// persistent waves per workgroup (one workgroup per CU, 3 waves per SIMD)
+// stream 16-token tiles as in window_qkv_stream_kernel: lane group q holds
+// channels [24 q, 24 q + 24) of its token (LayerNorm sums over the token's 4
+// lanes).  The output leaves in three chunks of 96 features (q, k, v);
+// within chunk c, lane group q computes features c * 96 + 24 q + [4 ft,
+// 4 ft + 4), staged through the wave's LDS slice and stored as 16-byte
+// vectors.
+constexpr int kLdsQkvWaves = 12;
+constexpr int kLdsQkvDepth = 2;  // tiles in flight per wave
+
+template <typename Tx, typename Tc, int kDepth>
+__global__ void __launch_bounds__(64 * kLdsQkvWaves)
+window_qkv_stream_lds_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln_w, const void* ln_b,
+                             int32_t ln_dtype, int32_t normalize, float eps, const Tc* __restrict__ w,
+                             const Tc* __restrict__ bias, const WinGeom g, uint32_t tiles) {
+    typedef typename Mma<Tc>::x4 X4;
+    typedef Tc T4 __attribute__((ext_vector_type(4)));
+    typedef Tx Tx4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t V16 __attribute__((ext_vector_type(4)));
+    constexpr int KS = 6, C = 16 * KS, NCH = 3, NOC = C, NO = NCH * NOC;
+    constexpr int kFtc = NOC / 16;           // feature tiles per chunk (6)
+    constexpr int kFrags = NCH * kFtc * KS;  // 108 A-operand fragments
+    constexpr int kThreadsL = 64 * kLdsQkvWaves;
+    constexpr int kPad = 8;
+    constexpr int kOutVecs = 16 * NOC / 8;  // 16-byte vectors per chunk of a tile
+    __shared__ __attribute__((aligned(16))) Tc w_lds[kFrags * 64 * 4];
+    __shared__ __attribute__((aligned(16))) Tc out_lds[kLdsQkvWaves][16 * (NOC + kPad)];
+    __shared__ __attribute__((aligned(16))) float par_lds[NO + 2 * C];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int col = lane & 15;
+    const int q = lane >> 4;
+    const uint32_t wgs = gridDim.x;  // a multiple of 8
+    const uint32_t wg = (blockIdx.x & 7u) * (wgs >> 3) + (blockIdx.x >> 3);
+    const uint32_t waves = wgs * kLdsQkvWaves;
+    const uint32_t L = wg * kLdsQkvWaves + wave;
+
+    // fragment j = (c * kFtc + ft) * KS + kk, lane (lc, lq): weight row
+    // c * 96 + 24 (lc >> 2) + 4 ft + (lc & 3), channels 24 lq + 4 kk .. + 3
+    for (int i = threadIdx.x; i < kFrags * 64; i += kThreadsL) {
+        const int j = i >> 6, l = i & 63;
+        const int kk = j % KS, cf = j / KS;
+        const int c = cf / kFtc, ft = cf - c * kFtc;
+        const int lc = l & 15, lq = l >> 4;
+        const int row = c * NOC + 24 * (lc >> 2) + 4 * ft + (lc & 3);
+        *reinterpret_cast<X4*>(&w_lds[4 * i]) = *reinterpret_cast<const X4*>(w + row * C + 24 * lq + 4 * kk);
+    }
+    for (int i = threadIdx.x; i < (NO + 2 * C) / 4; i += kThreadsL) {
+        f32x4 v;
+        if (4 * i < NO)
+            v = bias ? load4(bias + 4 * i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        else if (4 * i < NO + C)
+            v = load_param4(ln_w, ln_dtype, 4 * i - NO, 1.0f);
+        else
+            v = load_param4(ln_b, ln_dtype, 4 * i - NO - C, 0.0f);
+        *reinterpret_cast<f32x4*>(&par_lds[4 * i]) = v;
+    }
+    __syncthreads();  // weights and parameters are in LDS (every wave passes here once)
+    const float* gm_lds = par_lds + NO + 4 * KS * q;
+    const float* bt_lds = par_lds + NO + C + 4 * KS * q;
+
+    struct Raw {
+        Tx4 v[KS];
+        bool pad;
+    };
+    // the lane's channels of window-ordered token t (tiles clamped to the
+    // last, so that the loads are unconditional; padding reads row 0)
+    auto load_tile = [&](uint32_t t, Raw& r) {
+        const uint32_t tok = min(t, tiles - 1) * 16 + col;
+        const uint32_t row = tok < g.tokens ? token_row(tok, g) : kPadRow;
+        r.pad = row == kPadRow;
+        const Tx* src = x + int64_t(r.pad ? 0u : row) * C + 4 * KS * q;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) r.v[kk] = *reinterpret_cast<const Tx4*>(src + 4 * kk);
+    };
+    auto run_tile = [&](uint32_t t, const Raw& r) {
+        f32x4 v[KS];
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[kk][e] = r.pad ? 0.0f : to_f32(r.v[kk][e]);
+        if (normalize) {
+            float sm = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) sm += (v[kk][0] + v[kk][1]) + (v[kk][2] + v[kk][3]);
+            sm += __shfl_xor(sm, 16);
+            sm += __shfl_xor(sm, 32);
+            const float mean = sm / static_cast<float>(C);
+            float qs = 0.0f;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float dv = v[kk][e] - mean;
+                    qs = __builtin_fmaf(dv, dv, qs);
+                }
+            qs += __shfl_xor(qs, 16);
+            qs += __shfl_xor(qs, 32);
+            const float rstd = rsqrtf(qs / static_cast<float>(C) + eps);
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) {
+                const f32x4 gm = *reinterpret_cast<const f32x4*>(gm_lds + 4 * kk);
+                const f32x4 bt = *reinterpret_cast<const f32x4*>(bt_lds + 4 * kk);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    v[kk][e] = r.pad ? 0.0f : __builtin_fmaf((v[kk][e] - mean) * rstd, gm[e], bt[e]);
+            }
+        }
+        X4 xf[KS];
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xf[kk][e] = static_cast<Tc>(v[kk][e]);
+        Tc* ol = out_lds[wave];
+        const uint32_t t16 = t * 16;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+            wave_lds_sync();  // the previous chunk's vectors have been read
+#pragma unroll
+            for (int ft = 0; ft < kFtc; ++ft) {
+                f32x4 acc = *reinterpret_cast<const f32x4*>(par_lds + c * NOC + 24 * q + 4 * ft);
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) {
+                    const X4 wf = *reinterpret_cast<const X4*>(&w_lds[(((c * kFtc + ft) * KS + kk) * 64 + lane) * 4]);
+                    acc = Mma<Tc>::step(wf, xf[kk], acc);
+                }
+                T4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = static_cast<Tc>(acc[e]);
+                *reinterpret_cast<T4*>(&ol[col * (NOC + kPad) + 24 * q + 4 * ft]) = o;
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int it = 0; it < (kOutVecs + 63) / 64; ++it) {
+                const int i = lane + 64 * it;
+                const int tok = i / (NOC / 8);
+                const int part = i - tok * (NOC / 8);
+                if (i < kOutVecs && t16 + tok < g.tokens)
+                    __builtin_nontemporal_store(
+                        *reinterpret_cast<const V16*>(&ol[tok * (NOC + kPad) + 8 * part]),
+                        reinterpret_cast<V16*>(out + int64_t(t16 + tok) * NO + c * NOC + 8 * part));
+            }
+        }
+    };
+
+    Raw raw[kDepth];
+#pragma unroll
+    for (int d = 0; d < kDepth; ++d) load_tile(L + d * waves, raw[d]);
+    for (uint32_t t0 = L; t0 < tiles; t0 += kDepth * waves) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            const uint32_t t = t0 + d * waves;
+            if (t < tiles) {  // wave-uniform
+                run_tile(t, raw[d]);
+                load_tile(t + kDepth * waves, raw[d]);
+            }
+        }
+    }
+}
+
 int elem_size(int32_t dtype) {
     switch (dtype) {
         case CRUMPET_DTYPE_F32: return 4;
@@ -914,12 +1079,18 @@ bool qkv_streams(int32_t dtype, int64_t C, int64_t n_out) {
     return elem_size(dtype) == 2 && C <= 48 && n_out == 3 * C;
 }
 
+// 96 -> 288 (stage 1): the weights in LDS, one 12-wave workgroup per CU
+constexpr uint32_t kLdsQkvWorkgroups = 256;
+
+bool qkv_streams_lds(int32_t dtype, int64_t C, int64_t n_out) {
+    return elem_size(dtype) == 2 && C == 96 && n_out == 288;
+}
+
 // Grid of a streaming kernel: the fewest steps that `cap` workgroups allow,
 // then the fewest workgroups (a multiple of 8, one per XCD) that take every
 // tile in that many steps, so that the last step is nearly full for every
 // wave.
-dim3 stream_grid(uint32_t tiles, uint32_t cap) {
-    constexpr uint32_t kWaves = kThreads / 64;
+dim3 stream_grid(uint32_t tiles, uint32_t cap, uint32_t kWaves = kThreads / 64) {
     const uint32_t steps = std::max(1u, (tiles + cap * kWaves - 1) / (cap * kWaves));
     const uint32_t wgs = (tiles + steps * kWaves - 1) / (steps * kWaves);
     return dim3(std::max(8u, (wgs + 7) / 8 * 8));
@@ -951,6 +1122,27 @@ void launch_qkv_stream_x(int32_t dtype, int KS, hipStream_t s, void* out, const 
         launch_qkv_stream<Tx, _Float16>(KS, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
     else
         launch_qkv_stream<Tx, __bf16>(KS, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
+}
+
+template <typename Tx, typename Tc>
+void launch_qkv_stream_lds(hipStream_t s, void* out, const void* x, const void* ln_w, const void* ln_b,
+                           int32_t ln_dtype, int32_t normalize, float eps, const void* w, const void* bias,
+                           const WinGeom& g) {
+    const uint32_t tiles = (g.tokens + 15) / 16;
+    const dim3 grid = stream_grid(tiles, kLdsQkvWorkgroups, kLdsQkvWaves);
+    hipLaunchKernelGGL((window_qkv_stream_lds_kernel<Tx, Tc, kLdsQkvDepth>), grid, dim3(64 * kLdsQkvWaves), 0, s,
+                       static_cast<Tc*>(out), static_cast<const Tx*>(x), ln_w, ln_b, ln_dtype, normalize, eps,
+                       static_cast<const Tc*>(w), static_cast<const Tc*>(bias), g, tiles);
+}
+
+template <typename Tx>
+void launch_qkv_stream_lds_x(int32_t dtype, hipStream_t s, void* out, const void* x, const void* ln_w,
+                             const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps, const void* w,
+                             const void* bias, const WinGeom& g) {
+    if (dtype == CRUMPET_DTYPE_F16)
+        launch_qkv_stream_lds<Tx, _Float16>(s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
+    else
+        launch_qkv_stream_lds<Tx, __bf16>(s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
 }
 
 template <typename Tc, int KS>
@@ -1034,6 +1226,18 @@ extern "C" int crumpet_window_qkv_3d(void* out, int32_t dtype, const void* x, in
         else
             launch_qkv_stream_x<__bf16>(dtype, KS, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
                                         weight, bias, g);
+        return check_launch(what);
+    }
+    if (qkv_streams_lds(dtype, C, n_out)) {
+        if (x_dtype == CRUMPET_DTYPE_F32)
+            launch_qkv_stream_lds_x<float>(dtype, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps, weight,
+                                           bias, g);
+        else if (x_dtype == CRUMPET_DTYPE_F16)
+            launch_qkv_stream_lds_x<_Float16>(dtype, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                                              weight, bias, g);
+        else
+            launch_qkv_stream_lds_x<__bf16>(dtype, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                                            weight, bias, g);
         return check_launch(what);
     }
     if (x_dtype == CRUMPET_DTYPE_F32)
