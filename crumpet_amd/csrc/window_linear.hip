@@ -752,22 +752,25 @@ window_qkv_stream_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const v
     }
 }
 
-// window_qkv for 2-byte compute types at C = 96 (stage 1 of Swin UNETR at
-// feature size 48: 96 -> 288).  The 55 KB weight matrix does not fit a
-// wave's registers, so it sits in LDS for the whole launch in fragment
-// order: fragment (c, ft, kk) is 64 lanes x 4 elements, contiguous, so each
-// A-operand read is one conflict-free 8-byte LDS load per lane.  Twelve
-// persistent waves per workgroup (one workgroup per CU, 3 waves per SIMD)
-// stream 16-token tiles as in window_qkv_stream_kernel: lane group q holds
-// channels [24 q, 24 q + 24) of its token (LayerNorm sums over the token's 4
-// lanes).  The output leaves in three chunks of 96 features (q, k, v);
-// within chunk c, lane group q computes features c * 96 + 24 q + [4 ft,
-// 4 ft + 4), staged through the wave's LDS slice and stored as 16-byte
-// vectors.
+// window_qkv for 2-byte compute types at C = 96 and 192 (stages 1 and 2 of
+// Swin UNETR at feature size 48: 96 -> 288, 192 -> 576), whose weights do
+// not fit a wave's registers.  A workgroup holds NCH chunks of 96 output
+// features in LDS for the whole launch (stage 1 all three, 55 KB; stage 2
+// one of six, 37 KB), in fragment order: fragment (c, ft, kk) is 64 lanes x
+// 4 elements, contiguous, so each A-operand read is one conflict-free
+// 8-byte LDS load per lane.  Twelve persistent waves per workgroup (one
+// workgroup per CU, 3 waves per SIMD) stream 16-token tiles as in
+// window_qkv_stream_kernel: lane group q holds channels [4 KS q, 4 KS (q +
+// 1)) of its token (LayerNorm sums over the token's 4 lanes).  Chunk groups
+// alternate between neighbouring workgroups, which share an XCD and so read
+// the same tiles through one L2.  Within chunk c, lane group q computes
+// features c * 96 + 24 q + [4 ft, 4 ft + 4), staged through the wave's LDS
+// slice and stored as 16-byte vectors.
 constexpr int kLdsQkvWaves = 12;
-constexpr int kLdsQkvDepth = 2;  // tiles in flight per wave
+constexpr int kLdsQkvDepth = 2;  // tiles in flight per wave (C = 96; 1 at C = 192)
+constexpr int kLdsQkvChunk = 96;  // output features per chunk
 
-template <typename Tx, typename Tc, int kDepth>
+template <typename Tx, typename Tc, int KS, int NCH, int kDepth>
 __global__ void __launch_bounds__(64 * kLdsQkvWaves)
 window_qkv_stream_lds_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, const void* ln_w, const void* ln_b,
                              int32_t ln_dtype, int32_t normalize, float eps, const Tc* __restrict__ w,
@@ -776,47 +779,52 @@ window_qkv_stream_lds_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, con
     typedef Tc T4 __attribute__((ext_vector_type(4)));
     typedef Tx Tx4 __attribute__((ext_vector_type(4)));
     typedef uint32_t V16 __attribute__((ext_vector_type(4)));
-    constexpr int KS = 6, C = 16 * KS, NCH = 3, NOC = C, NO = NCH * NOC;
+    constexpr int C = 16 * KS, NOC = kLdsQkvChunk, NOW = NCH * NOC, NO = 3 * C;
+    constexpr int CG = NO / NOW;             // chunk groups
     constexpr int kFtc = NOC / 16;           // feature tiles per chunk (6)
-    constexpr int kFrags = NCH * kFtc * KS;  // 108 A-operand fragments
+    constexpr int kFrags = NCH * kFtc * KS;  // A-operand fragments held
     constexpr int kThreadsL = 64 * kLdsQkvWaves;
     constexpr int kPad = 8;
     constexpr int kOutVecs = 16 * NOC / 8;  // 16-byte vectors per chunk of a tile
+    static_assert(NO % NOW == 0 && NOC == 4 * 24, "chunk geometry");
     __shared__ __attribute__((aligned(16))) Tc w_lds[kFrags * 64 * 4];
     __shared__ __attribute__((aligned(16))) Tc out_lds[kLdsQkvWaves][16 * (NOC + kPad)];
-    __shared__ __attribute__((aligned(16))) float par_lds[NO + 2 * C];
+    __shared__ __attribute__((aligned(16))) float par_lds[NOW + 2 * C];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int col = lane & 15;
     const int q = lane >> 4;
-    const uint32_t wgs = gridDim.x;  // a multiple of 8
+    const uint32_t wgs = gridDim.x;  // a multiple of 8 and of CG
     const uint32_t wg = (blockIdx.x & 7u) * (wgs >> 3) + (blockIdx.x >> 3);
-    const uint32_t waves = wgs * kLdsQkvWaves;
-    const uint32_t L = wg * kLdsQkvWaves + wave;
+    const int cg = static_cast<int>(wg % CG);
+    const uint32_t waves = wgs / CG * kLdsQkvWaves;  // per chunk group
+    const uint32_t L = wg / CG * kLdsQkvWaves + wave;
+    const int f0 = cg * NOW;  // the workgroup's first output feature
 
     // fragment j = (c * kFtc + ft) * KS + kk, lane (lc, lq): weight row
-    // c * 96 + 24 (lc >> 2) + 4 ft + (lc & 3), channels 24 lq + 4 kk .. + 3
+    // f0 + c * 96 + 24 (lc >> 2) + 4 ft + (lc & 3), channels 4 KS lq + 4 kk .. + 3
     for (int i = threadIdx.x; i < kFrags * 64; i += kThreadsL) {
         const int j = i >> 6, l = i & 63;
         const int kk = j % KS, cf = j / KS;
         const int c = cf / kFtc, ft = cf - c * kFtc;
         const int lc = l & 15, lq = l >> 4;
-        const int row = c * NOC + 24 * (lc >> 2) + 4 * ft + (lc & 3);
-        *reinterpret_cast<X4*>(&w_lds[4 * i]) = *reinterpret_cast<const X4*>(w + row * C + 24 * lq + 4 * kk);
+        const int row = f0 + c * NOC + 24 * (lc >> 2) + 4 * ft + (lc & 3);
+        *reinterpret_cast<X4*>(&w_lds[4 * i]) =
+            *reinterpret_cast<const X4*>(w + row * C + 4 * KS * lq + 4 * kk);
     }
-    for (int i = threadIdx.x; i < (NO + 2 * C) / 4; i += kThreadsL) {
+    for (int i = threadIdx.x; i < (NOW + 2 * C) / 4; i += kThreadsL) {
         f32x4 v;
-        if (4 * i < NO)
-            v = bias ? load4(bias + 4 * i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-        else if (4 * i < NO + C)
-            v = load_param4(ln_w, ln_dtype, 4 * i - NO, 1.0f);
+        if (4 * i < NOW)
+            v = bias ? load4(bias + f0 + 4 * i) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        else if (4 * i < NOW + C)
+            v = load_param4(ln_w, ln_dtype, 4 * i - NOW, 1.0f);
         else
-            v = load_param4(ln_b, ln_dtype, 4 * i - NO - C, 0.0f);
+            v = load_param4(ln_b, ln_dtype, 4 * i - NOW - C, 0.0f);
         *reinterpret_cast<f32x4*>(&par_lds[4 * i]) = v;
     }
     __syncthreads();  // weights and parameters are in LDS (every wave passes here once)
-    const float* gm_lds = par_lds + NO + 4 * KS * q;
-    const float* bt_lds = par_lds + NO + C + 4 * KS * q;
+    const float* gm_lds = par_lds + NOW + 4 * KS * q;
+    const float* bt_lds = par_lds + NOW + C + 4 * KS * q;
 
     struct Raw {
         Tx4 v[KS];
@@ -897,7 +905,7 @@ window_qkv_stream_lds_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, con
                 if (i < kOutVecs && t16 + tok < g.tokens)
                     __builtin_nontemporal_store(
                         *reinterpret_cast<const V16*>(&ol[tok * (NOC + kPad) + 8 * part]),
-                        reinterpret_cast<V16*>(out + int64_t(t16 + tok) * NO + c * NOC + 8 * part));
+                        reinterpret_cast<V16*>(out + int64_t(t16 + tok) * NO + f0 + c * NOC + 8 * part));
             }
         }
     };
@@ -1079,18 +1087,20 @@ bool qkv_streams(int32_t dtype, int64_t C, int64_t n_out) {
     return elem_size(dtype) == 2 && C <= 48 && n_out == 3 * C;
 }
 
-// 96 -> 288 (stage 1): the weights in LDS, one 12-wave workgroup per CU
+// 96 -> 288 and 192 -> 576 (stages 1 and 2): the weights in LDS, one
+// 12-wave workgroup per CU
 constexpr uint32_t kLdsQkvWorkgroups = 256;
 
 bool qkv_streams_lds(int32_t dtype, int64_t C, int64_t n_out) {
-    return elem_size(dtype) == 2 && C == 96 && n_out == 288;
+    return elem_size(dtype) == 2 && (C == 96 || C == 192) && n_out == 3 * C;
 }
 
 // Grid of a streaming kernel: the fewest steps that `cap` workgroups allow,
 // then the fewest workgroups (a multiple of 8, one per XCD) that take every
 // tile in that many steps, so that the last step is nearly full for every
 // wave.
-dim3 stream_grid(uint32_t tiles, uint32_t cap, uint32_t kWaves = kThreads / 64) {
+dim3 stream_grid(uint32_t tiles, uint32_t cap) {
+    constexpr uint32_t kWaves = kThreads / 64;
     const uint32_t steps = std::max(1u, (tiles + cap * kWaves - 1) / (cap * kWaves));
     const uint32_t wgs = (tiles + steps * kWaves - 1) / (steps * kWaves);
     return dim3(std::max(8u, (wgs + 7) / 8 * 8));
@@ -1124,25 +1134,44 @@ void launch_qkv_stream_x(int32_t dtype, int KS, hipStream_t s, void* out, const 
         launch_qkv_stream<Tx, __bf16>(KS, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
 }
 
+// Per chunk group the fewest steps that its share of kLdsQkvWorkgroups
+// allows, then the fewest workgroups that take every tile in that many
+// steps; the total is a multiple of 8 (one per XCD) and of the chunk groups.
+template <typename Tx, typename Tc, int KS, int NCH, int kDepth>
+void launch_qkv_stream_lds_k(hipStream_t s, void* out, const void* x, const void* ln_w, const void* ln_b,
+                             int32_t ln_dtype, int32_t normalize, float eps, const void* w, const void* bias,
+                             const WinGeom& g) {
+    constexpr uint32_t CG = 3 * 16 * KS / (NCH * kLdsQkvChunk);
+    constexpr uint32_t kStep = CG % 8 == 0 ? 1 : (CG % 4 == 0 ? 2 : (CG % 2 == 0 ? 4 : 8));
+    const uint32_t tiles = (g.tokens + 15) / 16;
+    const uint32_t cap = std::max(1u, kLdsQkvWorkgroups / CG) * kLdsQkvWaves;  // waves per chunk group
+    const uint32_t steps = std::max(1u, (tiles + cap - 1) / cap);
+    uint32_t wpc = (tiles + steps * kLdsQkvWaves - 1) / (steps * kLdsQkvWaves);
+    wpc = (wpc + kStep - 1) / kStep * kStep;
+    hipLaunchKernelGGL((window_qkv_stream_lds_kernel<Tx, Tc, KS, NCH, kDepth>), dim3(CG * wpc),
+                       dim3(64 * kLdsQkvWaves), 0, s, static_cast<Tc*>(out), static_cast<const Tx*>(x), ln_w, ln_b,
+                       ln_dtype, normalize, eps, static_cast<const Tc*>(w), static_cast<const Tc*>(bias), g, tiles);
+}
+
 template <typename Tx, typename Tc>
-void launch_qkv_stream_lds(hipStream_t s, void* out, const void* x, const void* ln_w, const void* ln_b,
+void launch_qkv_stream_lds(int64_t C, hipStream_t s, void* out, const void* x, const void* ln_w, const void* ln_b,
                            int32_t ln_dtype, int32_t normalize, float eps, const void* w, const void* bias,
                            const WinGeom& g) {
-    const uint32_t tiles = (g.tokens + 15) / 16;
-    const dim3 grid = stream_grid(tiles, kLdsQkvWorkgroups, kLdsQkvWaves);
-    hipLaunchKernelGGL((window_qkv_stream_lds_kernel<Tx, Tc, kLdsQkvDepth>), grid, dim3(64 * kLdsQkvWaves), 0, s,
-                       static_cast<Tc*>(out), static_cast<const Tx*>(x), ln_w, ln_b, ln_dtype, normalize, eps,
-                       static_cast<const Tc*>(w), static_cast<const Tc*>(bias), g, tiles);
+    if (C == 96)  // all three chunks per workgroup (55 KB)
+        launch_qkv_stream_lds_k<Tx, Tc, 6, 3, kLdsQkvDepth>(s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w,
+                                                           bias, g);
+    else  // C = 192: one chunk of six per workgroup (37 KB)
+        launch_qkv_stream_lds_k<Tx, Tc, 12, 1, 1>(s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
 }
 
 template <typename Tx>
-void launch_qkv_stream_lds_x(int32_t dtype, hipStream_t s, void* out, const void* x, const void* ln_w,
+void launch_qkv_stream_lds_x(int32_t dtype, int64_t C, hipStream_t s, void* out, const void* x, const void* ln_w,
                              const void* ln_b, int32_t ln_dtype, int32_t normalize, float eps, const void* w,
                              const void* bias, const WinGeom& g) {
     if (dtype == CRUMPET_DTYPE_F16)
-        launch_qkv_stream_lds<Tx, _Float16>(s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
+        launch_qkv_stream_lds<Tx, _Float16>(C, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
     else
-        launch_qkv_stream_lds<Tx, __bf16>(s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
+        launch_qkv_stream_lds<Tx, __bf16>(C, s, out, x, ln_w, ln_b, ln_dtype, normalize, eps, w, bias, g);
 }
 
 template <typename Tc, int KS>
@@ -1230,13 +1259,13 @@ extern "C" int crumpet_window_qkv_3d(void* out, int32_t dtype, const void* x, in
     }
     if (qkv_streams_lds(dtype, C, n_out)) {
         if (x_dtype == CRUMPET_DTYPE_F32)
-            launch_qkv_stream_lds_x<float>(dtype, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps, weight,
-                                           bias, g);
+            launch_qkv_stream_lds_x<float>(dtype, C, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+                                           weight, bias, g);
         else if (x_dtype == CRUMPET_DTYPE_F16)
-            launch_qkv_stream_lds_x<_Float16>(dtype, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+            launch_qkv_stream_lds_x<_Float16>(dtype, C, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
                                               weight, bias, g);
         else
-            launch_qkv_stream_lds_x<__bf16>(dtype, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
+            launch_qkv_stream_lds_x<__bf16>(dtype, C, s, out, x, ln_weight, ln_bias, ln_dtype, normalize, eps,
                                             weight, bias, g);
         return check_launch(what);
     }

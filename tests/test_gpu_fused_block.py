@@ -114,15 +114,16 @@ def test_window_proj_matches_oracle(oracle, dev, case, cdt):
 
 
 @pytest.mark.parametrize("dts", DTYPES[:2] + DTYPES[3:], ids=lambda d: f"{NAME[d[0]]}-{NAME[d[1]]}")
-@pytest.mark.parametrize("C", [16, 32, 48, 96])
+@pytest.mark.parametrize("C", [16, 32, 48, 96, 192])
 @pytest.mark.parametrize("dims", [(1, 9, 10, 11), (1, 2, 3, 3)], ids=["9x10x11", "2x3x3"])
 def test_window_qkv_register_path(oracle, dev, dims, C, dts):
     """2-byte compute types with n_out = 3 C take the streaming kernels
     (LayerNorm statistics over the 4 lanes of a token, permuted contraction
     and feature order, 16-token tiles): C at most 48 with the weights in
-    registers, C = 96 with the weights in LDS and the output in q/k/v
-    chunks.  A partial last tile, fewer tiles than waves, LayerNorm off,
-    and LayerNorm parameters in the input's dtype."""
+    registers, C = 96 and 192 with the weights in LDS (all three q/k/v
+    chunks per workgroup, or one of six).  A partial last tile, fewer tiles
+    than waves, LayerNorm off, and LayerNorm parameters in the input's
+    dtype."""
     B, D, H, W = dims
     xdt, cdt = dts
     ws, ss = (7, 7, 7), (3, 3, 3)
@@ -167,23 +168,26 @@ def test_window_qkv_stage0_full_size(oracle, dev, cdt):
 
 
 @pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
-def test_window_qkv_stage1_full_size(oracle, dev, cdt):
-    """Config-5 stage 1 at full size on the LDS-weight streaming kernel: fp32
-    [4, 24^3, 96] -> [256, 343, 288] (5488 tiles, two steps of every wave),
-    every window-ordered token (padding included) against the oracle."""
-    B, D, C, ws, ss = 4, 24, 96, (7, 7, 7), (3, 3, 3)
+@pytest.mark.parametrize("D,C,nwin", [(24, 96, 256), (12, 192, 32)], ids=["s1", "s2"])
+def test_window_qkv_stages_1_2_full_size(oracle, dev, cdt, D, C, nwin):
+    """Config-5 stages 1 and 2 at full size on the LDS-weight streaming
+    kernel: fp32 [4, 24^3, 96] -> [256, 343, 288] (5488 tiles, two steps of
+    every wave, all three chunks per workgroup) and [4, 12^3, 192] ->
+    [32, 343, 576] (686 tiles in six chunk groups), every window-ordered
+    token (padding included) against the oracle."""
+    B, ws, ss = 4, (7, 7, 7), (3, 3, 3)
     x = seeded((B, D, D, D, C), torch.float32, 74) * 1.5 + 0.25
     gw = seeded((C,), torch.float32, 75) * 0.5 + 1.0
     gb = seeded((C,), torch.float32, 76) * 0.1
     w = (seeded((3 * C, C), torch.float32, 77) / C ** 0.5).to(cdt)
     b = (seeded((3 * C,), torch.float32, 78) * 0.1).to(cdt)
-    print(f"window_qkv stage 1 full size {cdt}", flush=True)
+    print(f"window_qkv full size C={C} {cdt}", flush=True)
     got = fused_block.window_qkv_3d(x.to(dev), w.to(dev), b.to(dev), ws, ss, gw.to(dev), gb.to(dev), 1e-5, True,
                                     cdt)
     want = oracle.window_qkv(x.double().numpy(), ws, ss, w.double().numpy(), b.double().numpy(),
                              gw.double().numpy(), gb.double().numpy(), 1e-5, True, NAME[cdt])
-    assert got.shape == want.shape == (256, 343, 288)
-    _compare(got, want, cdt, "window_qkv stage 1")
+    assert got.shape == want.shape == (nwin, 343, 3 * C)
+    _compare(got, want, cdt, f"window_qkv full size C={C}")
 
 
 @pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
