@@ -761,6 +761,19 @@ def profile_run(dev):
     ys = [torch.empty((4, 48, 48, 48, C0), dtype=torch.float16, device=dev) for _ in range(2)]
     timed("window_proj", lambda i: fused_block.window_proj_3d(wins[i % 2], wp, None, 4, 48, 48, 48, (7, 7, 7),
                                                               (3, 3, 3), ys[i % 2]))
+    del wins, ys
+    # window_qkv at the config-5 stage-1 and stage-2 shapes (the LDS-weight
+    # streaming kernel): fp32 [4,24^3,96] -> fp16 [256,343,288] and fp32
+    # [4,12^3,192] -> fp16 [32,343,576]; 2 rotating sets
+    for name, dim, cs, nwin in (("window_qkv_s1", 24, 96, 256), ("window_qkv_s2", 12, 192, 32)):
+        xs = [seeded((4, dim, dim, dim, cs), torch.float32, 140 + r).to(dev) for r in range(2)]
+        g1 = torch.ones(cs, device=dev)
+        b1 = torch.zeros(cs, device=dev)
+        w1 = (seeded((3 * cs, cs), torch.float32, 144) / cs ** 0.5).half().to(dev)
+        q1 = [torch.empty((nwin, 343, 3 * cs), dtype=torch.float16, device=dev) for _ in range(2)]
+        timed(name, lambda i: fused_block.window_qkv_3d(xs[i % 2], w1, None, (7, 7, 7), (3, 3, 3), g1, b1, 1e-5,
+                                                        True, torch.float16, q1[i % 2]))
+        del xs, q1
     print("profile sequence done", flush=True)
     print("PROFILE_EVENTS_US " + json.dumps(times), flush=True)
 
