@@ -243,14 +243,15 @@ def test_rows_8_byte_aligned(oracle, dev, dtype, masked):
     assert torch.isnan(out_buf[..., 16:].float()).all()  # nothing written past the head dim
 
 
-def test_config3_stage0_all_windows(oracle, dev):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_config3_stage0_all_windows(oracle, dev, dtype):
     """qkv [1372, 343, 144] fp16, table [2197, 3] trunc-normal 0.02,
     49^3 shifted mask tiled over sw-batch 4, scale 0.25.  Every window against
     the oracle, through the reference API (contiguous q/k/v, the mask
     repeated to [1372, N, N]: one head per workgroup) and through the
     window-batch entry the MONAI patch uses (q/k/v views of the qkv tensor,
-    the [343, N, N] mask read as mask[b mod 343] in mask-major window order)."""
-    dtype = torch.float16
+    the [343, N, N] mask read as mask[b mod 343] in mask-major window order);
+    in the BASELINE dtype fp16, and in bf16."""
     D, ws, ss = 49, (7, 7, 7), (3, 3, 3)
     B, H, N, Dh = 1372, 3, 343, 16
     qkv = seeded((B, N, 3 * H * Dh), dtype, 900)
@@ -321,11 +322,12 @@ def test_shifted_equals_tensor_mask_path(oracle, dev):
     assert (a.float() - b.float()).abs().max().item() <= 1e-3
 
 
-def test_config3_stage0_shifted_all_windows(oracle, dev):
-    """Config 3 through the region-mask path, every window vs the oracle."""
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["f16", "bf16"])
+def test_config3_stage0_shifted_all_windows(oracle, dev, dtype):
+    """Config 3 through the region-mask path, every window vs the oracle
+    (the BASELINE dtype fp16, and bf16)."""
     from crumpet_amd.fused_attention import fused_swin_attention_shifted
 
-    dtype = torch.float16
     D, ws, ss = 49, (7, 7, 7), (3, 3, 3)
     B, H, N, Dh = 1372, 3, 343, 16
     qkv = seeded((B, N, 3 * H * Dh), dtype, 1200)
