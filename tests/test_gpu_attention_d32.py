@@ -121,27 +121,25 @@ def test_tuned_and_general_kernels_agree(oracle, dev, dtype):
 
 
 @pytest.mark.parametrize("dtype", DT, ids=IDS)
-def test_config3_shape_sampled(oracle, dev, dtype):
+def test_config3_shape_all_windows(oracle, dev, dtype):
     """The config-3 window shape at head dim 32 (1372 windows x 3 heads of
     343 tokens, feature size 96), shifted mask of the 49^3 geometry as
-    region mode and as the [343] mask tensor with boundary flags: every
-    output finite, 49 windows of each checked against the oracle."""
+    region mode (three strip groups per workgroup) and as the [343] mask
+    tensor with boundary flags (4-wave workgroups): every window against
+    the oracle."""
     vol, ws, ss = (49, 49, 49), (7, 7, 7), (3, 3, 3)
     B, H, N = 1372, 3, 343
     _, q, k, v = _qkv_views(B, N, H, dtype, 5300)
     bias = bias_from_table(trunc_normal_table(13 ** 3, H, 5301), ws).to(dtype)
     m = torch.from_numpy(oracle.attn_mask(*vol, ws, ss, "float32"))
     bnd = boundary_flags(*vol, ws, ss, outer=4)
-    idx = np.arange(0, B, 28)
-    ref = oracle.attention(_f32(q[idx]), _f32(k[idx]), _f32(v[idx]), _f32(bias),
-                           m.numpy()[idx % 343], None, scale=0.25)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m.numpy(), None, scale=0.25)  # mask[b % 343]
     qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
     out_r = fused_swin_attention_shifted(qd, kd, vd, bias.to(dev), vol, ws, ss, 0.25)
     out_t = fused_swin_attention_windows(qd, kd, vd, bias.to(dev), m.to(dtype).to(dev), bnd.to(dev), 0.25,
                                          torch.empty((B, H, N, 32), dtype=dtype, device=dev))
     for name, out in (("region", out_r), ("tensor", out_t)):
-        assert torch.isfinite(out.float()).all()
-        _compare(out[torch.from_numpy(idx).to(dev)], ref, dtype, f"config-3 shape d32 {name} {dtype}")
+        _compare(out, ref, dtype, f"config-3 shape d32 {name} {dtype}")
 
 
 @pytest.mark.parametrize("dtype", DT, ids=IDS)
