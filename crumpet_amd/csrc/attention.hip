@@ -267,7 +267,6 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.chunks = static_cast<uint32_t>(chunks);
     p.launched = xcd_launch_count(p.chunks);
 
-
     if (tuned32)
         attn::launch_d32(p, NT, kmask, dtype, s);
     else if (dtype == CRUMPET_DTYPE_F16)
