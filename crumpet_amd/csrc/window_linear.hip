@@ -803,14 +803,25 @@ window_qkv_stream_lds_kernel(Tc* __restrict__ out, const Tx* __restrict__ x, con
 
     // fragment j = (c * kFtc + ft) * KS + kk, lane (lc, lq): weight row
     // f0 + c * 96 + 24 (lc >> 2) + 4 ft + (lc & 3), channels 4 KS lq + 4 kk .. + 3
-    for (int i = threadIdx.x; i < kFrags * 64; i += kThreadsL) {
-        const int j = i >> 6, l = i & 63;
-        const int kk = j % KS, cf = j / KS;
-        const int c = cf / kFtc, ft = cf - c * kFtc;
-        const int lc = l & 15, lq = l >> 4;
-        const int row = f0 + c * NOC + 24 * (lc >> 2) + 4 * ft + (lc & 3);
-        *reinterpret_cast<X4*>(&w_lds[4 * i]) =
-            *reinterpret_cast<const X4*>(w + row * C + 4 * KS * lq + 4 * kk);
+    // (every load of the fill is issued before the first store waits)
+    constexpr int kFill = (kFrags * 64 + kThreadsL - 1) / kThreadsL;
+    X4 wtmp[kFill];
+#pragma unroll
+    for (int it = 0; it < kFill; ++it) {
+        const int i = static_cast<int>(threadIdx.x) + it * kThreadsL;
+        if (i < kFrags * 64) {
+            const int j = i >> 6, l = i & 63;
+            const int kk = j % KS, cf = j / KS;
+            const int c = cf / kFtc, ft = cf - c * kFtc;
+            const int lc = l & 15, lq = l >> 4;
+            const int row = f0 + c * NOC + 24 * (lc >> 2) + 4 * ft + (lc & 3);
+            wtmp[it] = *reinterpret_cast<const X4*>(w + row * C + 4 * KS * lq + 4 * kk);
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < kFill; ++it) {
+        const int i = static_cast<int>(threadIdx.x) + it * kThreadsL;
+        if (i < kFrags * 64) *reinterpret_cast<X4*>(&w_lds[4 * i]) = wtmp[it];
     }
     for (int i = threadIdx.x; i < (NOW + 2 * C) / 4; i += kThreadsL) {
         f32x4 v;
