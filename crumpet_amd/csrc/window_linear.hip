@@ -32,11 +32,13 @@
 // consecutive output features of one token; they go to an LDS output chunk
 // that the workgroup writes back as consecutive 16-byte vectors.
 // With a 2-byte compute type and small C (stage 0), window_proj (C and
-// n_out at most 64) and window_qkv (n_out = 3 C, C at most 48) take
-// window_proj_stream_kernel / window_qkv_stream_kernel instead: independent
-// persistent waves with the weights in registers (stage 0: 74% and 77% of
-// HBM against 60% and 69% for the tiled kernels, whose workgroups drain the
-// memory queue at every barrier).
+// n_out at most 64, or 96 -> 96) and window_qkv (n_out = 3 C, C at most 48)
+// take window_proj_stream_kernel / window_qkv_stream_kernel instead:
+// independent persistent waves with the weights in registers (stage 0: 74%
+// and 77% of HBM against 60% and 69% for the tiled kernels, whose
+// workgroups drain the memory queue at every barrier).  window_qkv at C = 96
+// and 192 (stages 1 and 2) takes window_qkv_stream_lds_kernel: the same
+// persistent waves, with the weights in LDS.
 //
 // Numerics: LayerNorm in fp32 (two passes: mean, then the mean of squared
 // deviations; biased variance, as torch), the normalised value rounded once
