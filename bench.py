@@ -150,7 +150,24 @@ def bench_partition(args, dev):
     t_part = _steady_time(part, args.warmup, args.steps, dev)
     t_unpart = _steady_time(unpart, args.warmup, args.steps, dev)
     t_step = _steady_time(step, args.warmup, args.steps, dev)
-    return dict(t_part=t_part, t_unpart=t_unpart, t_step=t_step)
+
+    # the reference's eager path on the same GPU (torch.roll + the MONAI
+    # view/permute window partition, and window reverse + roll back), the
+    # comparison its own speedup figures make
+    from crumpet_amd import swin_unetr_compat as sw
+
+    def eager_part(i):
+        sw.window_partition(torch.roll(xs[i % R], tuple(-s for s in ss), (1, 2, 3)), ws)
+
+    def eager_unpart(i):
+        torch.roll(sw.window_reverse(wins[i % R], ws, (B, D, H, W)), ss, (1, 2, 3))
+
+    assert torch.equal(sw.window_partition(torch.roll(xs[0], tuple(-s for s in ss), (1, 2, 3)), ws),
+                       crumpet_amd.fused_shift_partition_3d(xs[0], ws, ss))
+    t_eager_part = _steady_time(eager_part, args.warmup, args.steps, dev)
+    t_eager_unpart = _steady_time(eager_unpart, args.warmup, args.steps, dev)
+    return dict(t_part=t_part, t_unpart=t_unpart, t_step=t_step, t_eager_part=t_eager_part,
+                t_eager_unpart=t_eager_unpart)
 
 
 def bench_mask(args, dev):
@@ -162,7 +179,19 @@ def bench_mask(args, dev):
     def mk(i):
         ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
 
-    return _steady_time(mk, args.warmup, args.steps, dev)
+    t = _steady_time(mk, args.warmup, args.steps, dev)
+    # the MONAI slice-assignment construction (benchmarks/bench_kernel.py:63-86
+    # in the reference) on the same GPU, fp32 then cast, as its speedup
+    # figures compare; bit-identical to the kernel's output
+    from crumpet_amd import swin_unetr_compat as sw
+
+    def eager(i):
+        sw.compute_mask((98, 98, 98), (7, 7, 7), (3, 3, 3), dev).to(torch.float16)
+
+    assert torch.equal(sw.compute_mask((98, 98, 98), (7, 7, 7), (3, 3, 3), dev).to(torch.float16), out)
+    t_eager = _steady_time(eager, 1, 5, dev)
+    torch.cuda.empty_cache()
+    return t, t_eager
 
 
 def c3_inputs(dev, sets):
@@ -811,7 +840,7 @@ def main():
         return
 
     p = bench_partition(args, dev)
-    t_mask = bench_mask(args, dev)
+    t_mask, t_mask_eager = bench_mask(args, dev)
     torch.cuda.empty_cache()
     a = {} if args.no_attention else bench_attention(args, dev)
     torch.cuda.empty_cache()
@@ -830,11 +859,16 @@ def main():
     gbs_mask = C2_BYTES / (t_mask * 1e-3) / 1e9
     components = {
         "partition": {"ms": round(p["t_part"], 5), "GB_s": round(gbs_part, 1),
-                      "frac_hbm": round(gbs_part / HBM_PEAK_GBS, 4), "bytes": C1_BYTES},
+                      "frac_hbm": round(gbs_part / HBM_PEAK_GBS, 4), "bytes": C1_BYTES,
+                      "eager_rocm_ms": round(p["t_eager_part"], 4),
+                      "speedup_vs_eager": round(p["t_eager_part"] / p["t_part"], 2)},
         "unpartition": {"ms": round(p["t_unpart"], 5), "GB_s": round(gbs_unpart, 1),
-                        "frac_hbm": round(gbs_unpart / HBM_PEAK_GBS, 4), "bytes": C1_BYTES},
+                        "frac_hbm": round(gbs_unpart / HBM_PEAK_GBS, 4), "bytes": C1_BYTES,
+                        "eager_rocm_ms": round(p["t_eager_unpart"], 4),
+                        "speedup_vs_eager": round(p["t_eager_unpart"] / p["t_unpart"], 2)},
         "mask": {"ms": round(t_mask, 5), "GB_s": round(gbs_mask, 1),
                  "frac_hbm": round(gbs_mask / HBM_PEAK_GBS, 4), "bytes": C2_BYTES,
+                 "eager_rocm_ms": round(t_mask_eager, 3), "speedup_vs_eager": round(t_mask_eager / t_mask, 1),
                  "workload": "config 2: 98^3 fp16 ws7 ss3 -> [2744,343,343]"},
     }
     if a:
