@@ -151,23 +151,7 @@ def bench_partition(args, dev):
     t_unpart = _steady_time(unpart, args.warmup, args.steps, dev)
     t_step = _steady_time(step, args.warmup, args.steps, dev)
 
-    # the reference's eager path on the same GPU (torch.roll + the MONAI
-    # view/permute window partition, and window reverse + roll back), the
-    # comparison its own speedup figures make
-    from crumpet_amd import swin_unetr_compat as sw
-
-    def eager_part(i):
-        sw.window_partition(torch.roll(xs[i % R], tuple(-s for s in ss), (1, 2, 3)), ws)
-
-    def eager_unpart(i):
-        torch.roll(sw.window_reverse(wins[i % R], ws, (B, D, H, W)), ss, (1, 2, 3))
-
-    assert torch.equal(sw.window_partition(torch.roll(xs[0], tuple(-s for s in ss), (1, 2, 3)), ws),
-                       crumpet_amd.fused_shift_partition_3d(xs[0], ws, ss))
-    t_eager_part = _steady_time(eager_part, args.warmup, args.steps, dev)
-    t_eager_unpart = _steady_time(eager_unpart, args.warmup, args.steps, dev)
-    return dict(t_part=t_part, t_unpart=t_unpart, t_step=t_step, t_eager_part=t_eager_part,
-                t_eager_unpart=t_eager_unpart)
+    return dict(t_part=t_part, t_unpart=t_unpart, t_step=t_step)
 
 
 def bench_mask(args, dev):
@@ -179,19 +163,52 @@ def bench_mask(args, dev):
     def mk(i):
         ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
 
-    t = _steady_time(mk, args.warmup, args.steps, dev)
-    # the MONAI slice-assignment construction (benchmarks/bench_kernel.py:63-86
-    # in the reference) on the same GPU, fp32 then cast, as its speedup
-    # figures compare; bit-identical to the kernel's output
+    return _steady_time(mk, args.warmup, args.steps, dev)
+
+
+def bench_eager_references(args, dev):
+    """The reference's eager constructions for configs 1 and 2 on the same
+    GPU, the comparison its own speedup figures make: torch.roll + the MONAI
+    view/permute window partition and window reverse + roll back
+    (torch-ext/crumpet/reference.py:141-184), and the MONAI slice-assignment
+    mask (benchmarks/bench_kernel.py:63-86), fp32 then cast.  Each is first
+    checked equal to the kernel's output.  Timed after every fused
+    measurement: the eager constructions' large temporaries left fused
+    launches measured after them slower."""
+    import torch
+
+    import crumpet_amd
     from crumpet_amd import swin_unetr_compat as sw
 
-    def eager(i):
+    B, D, H, W, C, ws, ss = (C1[k] for k in ("B", "D", "H", "W", "C", "ws", "ss"))
+    R = 2
+    xs = [seeded((B, D, H, W, C), torch.float16, 100 + r).to(dev) for r in range(R)]
+    wins = [crumpet_amd.fused_shift_partition_3d(x, ws, ss) for x in xs]
+    neg = tuple(-v for v in ss)
+    assert torch.equal(sw.window_partition(torch.roll(xs[0], neg, (1, 2, 3)), ws), wins[0])
+    assert torch.equal(torch.roll(sw.window_reverse(wins[0], ws, (B, D, H, W)), ss, (1, 2, 3)), xs[0])
+
+    def eager_part(i):
+        sw.window_partition(torch.roll(xs[i % R], neg, (1, 2, 3)), ws)
+
+    def eager_unpart(i):
+        torch.roll(sw.window_reverse(wins[i % R], ws, (B, D, H, W)), ss, (1, 2, 3))
+
+    res = {"t_eager_part": _steady_time(eager_part, 3, 10, dev),
+           "t_eager_unpart": _steady_time(eager_unpart, 3, 10, dev)}
+    del xs, wins
+    torch.cuda.empty_cache()
+    out = torch.empty((2744, 343, 343), dtype=torch.float16, device=dev)
+    torch.ops.crumpet_ops.compute_attn_mask_3d(out, 98, 98, 98, 7, 7, 7, 3, 3, 3)
+    assert torch.equal(sw.compute_mask((98, 98, 98), (7, 7, 7), (3, 3, 3), dev).to(torch.float16), out)
+    del out
+
+    def eager_mask(i):
         sw.compute_mask((98, 98, 98), (7, 7, 7), (3, 3, 3), dev).to(torch.float16)
 
-    assert torch.equal(sw.compute_mask((98, 98, 98), (7, 7, 7), (3, 3, 3), dev).to(torch.float16), out)
-    t_eager = _steady_time(eager, 1, 5, dev)
+    res["t_eager_mask"] = _steady_time(eager_mask, 1, 5, dev)
     torch.cuda.empty_cache()
-    return t, t_eager
+    return res
 
 
 def c3_inputs(dev, sets):
@@ -357,9 +374,10 @@ def bench_blocks(args, dev):
     from crumpet_amd.fused_attention import fused_swin_attention_shifted
 
     res = {}
+    eager_jobs = []
+    B = 4
     for dtype, tag in ((torch.float16, "fp16"), (torch.bfloat16, "bf16")):
         for name, dim, C, H, ws, ss in STAGES:
-            B = 4
             x = seeded((B, dim, dim, dim, C), dtype, 500 + dim).to(dev)
             N = ws[0] * ws[1] * ws[2]
             g = torch.Generator().manual_seed(510 + dim)
@@ -393,6 +411,7 @@ def bench_blocks(args, dev):
                 step(0)
             ms_graph = _steady_time(lambda i: graph.replay(), args.warmup, args.steps, dev)
             del graph
+            eager_jobs.append((f"{name}_{tag}", x, bias, dtype, dim, C, H, ws, ss, N))
             tokens = B * dim ** 3
             part_bytes = 2 * tokens * C * x.element_size()
             flops = 4 * N * N * 16 * H * (tokens // N)
@@ -401,7 +420,39 @@ def bench_blocks(args, dev):
                                     "window": list(ws), "shift": list(ss),
                                     "partition_bytes": part_bytes, "attention_flops": flops,
                                     "effective_GB_s": round(3 * part_bytes / (ms * 1e-3) / 1e9, 1)}
-            del x
+
+    # the eager chain on the same GPU, after every fused measurement (its
+    # large temporaries left eager fused launches measured after it several
+    # times slower): roll + window partition, the MONAI attention chain (mask
+    # from compute_mask, cached as MONAI's BasicLayer does), window reverse +
+    # roll back
+    from crumpet_amd import swin_unetr_compat as sw
+
+    for key, x, bias, dtype, dim, C, H, ws, ss, N in eager_jobs:
+        shifted = any(ss)
+        emask = sw.compute_mask((dim,) * 3, ws, ss, dev).to(dtype) if shifted else None
+
+        def eager_step(i):
+            xr = torch.roll(x, tuple(-v for v in ss), (1, 2, 3)) if shifted else x
+            w = sw.window_partition(xr, ws)
+            nwin = w.shape[0]
+            t = w.view(nwin, N, H, 16).permute(0, 2, 1, 3)
+            a = (t * 0.25) @ t.transpose(-2, -1).contiguous() + bias.unsqueeze(0)
+            if shifted:
+                nw = emask.shape[0]
+                a = (a.view(nwin // nw, nw, H, N, N) + emask.unsqueeze(1).unsqueeze(0)).view(-1, H, N, N)
+            o = (torch.softmax(a, dim=-1) @ t).transpose(1, 2).reshape(nwin, N, C)
+            back = sw.window_reverse(o, ws, (B, dim, dim, dim))
+            return torch.roll(back, ss, (1, 2, 3)) if shifted else back
+
+        with torch.no_grad():
+            ms_eager = _steady_time(eager_step, 2, max(3, min(args.steps, 10)), dev)
+        res[key]["eager_rocm_ms"] = round(ms_eager, 4)
+        res[key]["speedup_vs_eager"] = round(ms_eager / res[key]["ms"], 2)
+        res[key]["speedup_vs_eager_graph"] = round(ms_eager / res[key]["ms_graph_replay"], 2)
+        del emask
+    del eager_jobs
+    torch.cuda.empty_cache()
     return res
 
 
@@ -840,7 +891,7 @@ def main():
         return
 
     p = bench_partition(args, dev)
-    t_mask, t_mask_eager = bench_mask(args, dev)
+    t_mask = bench_mask(args, dev)
     torch.cuda.empty_cache()
     a = {} if args.no_attention else bench_attention(args, dev)
     torch.cuda.empty_cache()
@@ -852,6 +903,7 @@ def main():
     torch.cuda.empty_cache()
     e2e = {} if args.no_e2e else bench_e2e(args, dev)
     torch.cuda.empty_cache()
+    eager_refs = bench_eager_references(args, dev)
 
     gbs_step = 2 * C1_BYTES / (p["t_step"] * 1e-3) / 1e9
     gbs_part = C1_BYTES / (p["t_part"] * 1e-3) / 1e9
@@ -860,15 +912,16 @@ def main():
     components = {
         "partition": {"ms": round(p["t_part"], 5), "GB_s": round(gbs_part, 1),
                       "frac_hbm": round(gbs_part / HBM_PEAK_GBS, 4), "bytes": C1_BYTES,
-                      "eager_rocm_ms": round(p["t_eager_part"], 4),
-                      "speedup_vs_eager": round(p["t_eager_part"] / p["t_part"], 2)},
+                      "eager_rocm_ms": round(eager_refs["t_eager_part"], 4),
+                      "speedup_vs_eager": round(eager_refs["t_eager_part"] / p["t_part"], 2)},
         "unpartition": {"ms": round(p["t_unpart"], 5), "GB_s": round(gbs_unpart, 1),
                         "frac_hbm": round(gbs_unpart / HBM_PEAK_GBS, 4), "bytes": C1_BYTES,
-                        "eager_rocm_ms": round(p["t_eager_unpart"], 4),
-                        "speedup_vs_eager": round(p["t_eager_unpart"] / p["t_unpart"], 2)},
+                        "eager_rocm_ms": round(eager_refs["t_eager_unpart"], 4),
+                        "speedup_vs_eager": round(eager_refs["t_eager_unpart"] / p["t_unpart"], 2)},
         "mask": {"ms": round(t_mask, 5), "GB_s": round(gbs_mask, 1),
                  "frac_hbm": round(gbs_mask / HBM_PEAK_GBS, 4), "bytes": C2_BYTES,
-                 "eager_rocm_ms": round(t_mask_eager, 3), "speedup_vs_eager": round(t_mask_eager / t_mask, 1),
+                 "eager_rocm_ms": round(eager_refs["t_eager_mask"], 3),
+                 "speedup_vs_eager": round(eager_refs["t_eager_mask"] / t_mask, 1),
                  "workload": "config 2: 98^3 fp16 ws7 ss3 -> [2744,343,343]"},
     }
     if a:
