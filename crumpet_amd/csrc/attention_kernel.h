@@ -274,6 +274,7 @@ struct Frag<__bf16> {
 template <>
 struct Frag<float> {
     typedef f32x4 x4;
+    typedef f32x4 x8;  // unused: fp32 operands take four 16x16x4 steps, no 8-element fragments
 };
 
 // 4 consecutive head-dim elements (d0..d0+3) of one row: one vector load
@@ -303,11 +304,12 @@ __device__ __forceinline__ typename Frag<T>::x4 scaled(typename Frag<T>::x4 v, f
     return v;
 }
 
-// Four dims of a Q row into LDS at row + d0.  2-byte types store
-// hi = q * scale rounded (scale includes log2(e)) at d0 and the remainder
-// lo = q * scale - hi, rounded, at 16 + d0: hi + lo carries q * scale to
-// about twice the input precision, so folding log2(e) into the operand adds
-// no rounding of its own.  fp32 stores q * scale.
+// Four dims d0 .. d0 + 3 of a Q row into LDS.  2-byte types store
+// hi = q * scale rounded (scale includes log2(e)) and the remainder
+// lo = q * scale - hi, rounded: hi + lo carries q * scale to about twice the
+// input precision, so folding log2(e) into the operand adds no rounding of
+// its own.  The row holds [hi 0-7 | lo 0-7 | hi 8-15 | lo 8-15] (the k-slices
+// of the score product, q_slice).  fp32 stores q * scale.
 template <typename T>
 __device__ __forceinline__ void store_q4(T* row, int d0, typename Frag<T>::x4 v, float scale) {
     typedef typename Frag<T>::x4 X4;
@@ -319,18 +321,19 @@ __device__ __forceinline__ void store_q4(T* row, int d0, typename Frag<T>::x4 v,
             hi[e] = T(x);
             lo[e] = T(x - static_cast<float>(hi[e]));
         }
-        *reinterpret_cast<X4*>(row + d0) = hi;
-        *reinterpret_cast<X4*>(row + 16 + d0) = lo;
+        *reinterpret_cast<X4*>(row + (d0 >> 3) * 16 + (d0 & 7)) = hi;
+        *reinterpret_cast<X4*>(row + (d0 >> 3) * 16 + 8 + (d0 & 7)) = lo;
     } else {
         *reinterpret_cast<X4*>(row + d0) = scaled<T>(v, scale);
     }
 }
 
 // K layout in LDS.  2-byte types: each 16-row key tile stores the first 8
-// dims of its 16 rows (16 B each), then the last 8, so the lanes 0-31 that
-// read one 16x16x32 key fragment (row col, dims 8g..8g+7, g = 0, 1) cover
-// 512 contiguous bytes (lanes 32-63 read the same bytes again: the score
-// product repeats K in its dims 16-31, attend_offset).  fp32: plain rows.
+// dims of its 16 rows (16 B each), then the last 8, so a 16x16x32 key
+// fragment (lane (col, g): row col, dims 8(g >> 1) .. + 7; the score product
+// carries each 8 dims twice, for Q_hi and Q_lo, attend_offset) reads 256
+// contiguous bytes with lanes 0-31 and the next 256 with lanes 32-63.  fp32:
+// plain rows.
 template <typename T>
 __device__ __forceinline__ constexpr int kidx(int row, int d) {
     if constexpr (sizeof(T) == 2)
@@ -341,7 +344,7 @@ __device__ __forceinline__ constexpr int kidx(int row, int d) {
 
 // Head dim 32 (2-byte types): a Q row holds 64 elements, hi = q * scale
 // rounded (dims 0-31; scale includes log2(e)) and lo = the rounding
-// remainder (32-63), as store_q4 does for head dim 16; each score tile then
+// remainder (32-63), the split store_q4 makes for head dim 16; each score tile then
 // takes two 16x16x32 products over the same K fragment (Q_hi, then Q_lo),
 // since the head dim fills the product's depth.  A key tile stores dims
 // 8c .. 8c + 7 of its 16 rows as block c = 0..3 (16 B per row), so the lanes
@@ -632,15 +635,26 @@ __device__ __forceinline__ u32x4 desc_words(const void* base, int64_t off, int64
 // before unrelated LDS reads; the caller waits (vmcnt(0)) before the barrier
 // that publishes the rows.  The LDS address enters as an operand bound to
 // M0, so the compiler writes M0 itself and knows it is live (a clobber of
-// the reserved M0 would not be honoured).  gfx950 needs one wait state
-// between an SALU write of M0 and an LDS-DMA load that reads it; the
-// compiler's hazard recognizer does not look inside inline asm, hence the
-// s_nop ahead of the load.
+// the reserved M0 would not be honoured).  The compiler's hazard recognizer
+// does not look inside inline asm, so the asm carries the wait states its
+// load needs: one after an SALU write of M0, and five after a VALU write of
+// an SGPR of the descriptor.  The second happens when the compiler restores
+// a spilled descriptor with v_readlane right before the load: with one wait
+// state the load read a stale descriptor word and fetched wrong rows (the
+// head-dim-16 bf16 kernel at 14 tiles, which spills scalar registers).
 __device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, int voff) {
-    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+    asm volatile("s_nop 4\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
                  : "v"(voff), "s"(desc), "{m0}"(lds_addr)
                  : "memory");
+}
+
+// s_waitcnt vmcnt(0) through the builtin: the compiler's wait insertion
+// then knows that every vector-memory request issued before it, its own
+// and the LDS-DMA loads it cannot see, has completed, and adds no wait of
+// its own for registers loaded earlier.
+__device__ __forceinline__ void wait_vmem() {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0) expcnt(7) lgkmcnt(15)
 }
 
 template <typename T, int D>
@@ -1009,8 +1023,9 @@ __device__ __forceinline__ float xmax32(float m) {
 // Scores come out of the score product in log2 units, so that P = 2^S needs
 // no multiply-add: the bias (+ region mask) tiles are kept multiplied by
 // log2(e), and Q by scale * log2(e).  Q enters the 16x16x32 product as
-// hi + lo (store_q4): dims 0-15 carry K . Q_hi, dims 16-31 (K repeated)
-// K . Q_lo, so the folded log2(e) adds no rounding beyond fp32.
+// hi + lo (store_q4): its k-slices 8s .. 8s + 7 carry K . Q_hi (s even) and
+// K . Q_lo (s odd) over dims 8(s >> 1) .. + 7, K repeated, so the folded
+// log2(e) adds no rounding beyond fp32.
 //
 // No row max is taken.  The bias tiles carry a per-query offset instead
 // (build_tiles), and softmax is invariant to it, so the offset only has to
@@ -1074,11 +1089,88 @@ struct NoIssue {
     __device__ __forceinline__ void operator()(int) const {}
 };
 
-template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, int D, typename Issue>
-__device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const T* __restrict__ q_lds,
-                                              const T* __restrict__ k_lds, const T* __restrict__ v_lds, int b,
-                                              int h, int wave, int qi, int col, int g, float& off,
-                                              const Issue& issue) {
+// One strip's normalised output, held back for a deferred store (vector IO,
+// head dim 16): a wave writes window i's output at the top of window i + 1.
+// The vector-memory counter retires stores with the loads, so a store issued
+// at the end of window i would be waited for by the wait on window i + 1's
+// rows that ends the window; issued a window earlier it has long completed.
+template <typename T>
+struct PendingOut {
+    typename Frag<T>::x4 r;  // O[qi][4g .. 4g + 3]
+};
+
+template <typename T>
+__device__ __forceinline__ void store_out4(const Params& p, const typename Frag<T>::x4& r, int b, int h, int qi,
+                                           int g) {
+    if (qi < p.N) {
+        T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
+        *reinterpret_cast<typename Frag<T>::x4*>(orow + 4 * g) = r;
+    }
+}
+
+// Head dim 16, LDS-DMA path: a wave's Q operand never passes through LDS.
+// Lane (col, g) loads the 8 raw elements of dims 8(g >> 1) .. + 7 of its
+// query row (clamped to N - 1; padded rows are never stored) from the
+// window's Q rows, and q_operand turns them into the k-slice g of the score
+// product: hi = q * scale rounded for even g, the remainder lo for odd g
+// (store_q4 makes the same split).
+template <typename T>
+struct QRaw {
+    u32x2 w[2];  // 8 elements of T
+};
+
+template <typename T>
+__device__ __forceinline__ QRaw<T> load_qraw(const Params& p, int b, int h, int qi, int g) {
+    const int N = p.N;
+    char* ub = uniform_ptr(static_cast<const char*>(p.q) + (int64_t(b) * p.qs[0] + int64_t(h) * p.qs[1]) *
+                                                            int64_t(sizeof(T)));
+    const int extent = __builtin_amdgcn_readfirstlane(
+        static_cast<int>((int64_t(N - 1) * p.qs[2] + 16) * int64_t(sizeof(T))));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(ub, 0, extent, 0x00020000);
+    const int off = (min(qi, N - 1) * static_cast<int>(p.qs[2]) + 8 * (g >> 1)) * static_cast<int>(sizeof(T));
+    QRaw<T> r;
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+    r.w[1] = __builtin_amdgcn_raw_buffer_load_b64(rs, off + 8, 0, 0);
+    return r;
+}
+
+template <typename T>
+__device__ __forceinline__ typename Frag<T>::x8 q_operand(const QRaw<T>& raw, float scale, int g) {
+    typedef typename Frag<T>::x4 X4;
+    const X4 a = __builtin_bit_cast(X4, raw.w[0]);
+    const X4 c = __builtin_bit_cast(X4, raw.w[1]);
+    const bool lo = g & 1;
+    typename Frag<T>::x8 r;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float x = static_cast<float>(e < 4 ? a[e] : c[e - 4]) * scale;
+        const T hi = T(x);
+        r[e] = lo ? T(x - static_cast<float>(hi)) : hi;
+    }
+    return r;
+}
+
+// Wave priority by progress through a window's tile pairs: 3 in the first
+// quarter of the pairs down to 0 in the last.  The arbiter otherwise issues
+// for the oldest wave of a SIMD first, so the three waves of a SIMD finished
+// a window up to a third of its compute apart, and the youngest ran its last
+// pairs alone, with its dependency stalls exposed; ranking by progress keeps
+// the three in step (config 3 shifted: 119 -> 113 us).
+__device__ __forceinline__ void set_wave_prio(int level) {
+    switch (level) {  // the builtin takes a constant; level is one after unrolling
+        case 0: __builtin_amdgcn_s_setprio(0); break;
+        case 1: __builtin_amdgcn_s_setprio(1); break;
+        case 2: __builtin_amdgcn_s_setprio(2); break;
+        default: __builtin_amdgcn_s_setprio(3); break;
+    }
+}
+
+template <typename T, int NT, int kMask, bool kUseMask, bool kVec, bool kRec, int D, bool kDefer, typename Issue>
+__device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)[NT], const typename Frag<T>::x8& qf,
+                                              const typename Frag<T>::x8& qf_lo, const T* __restrict__ k_lds,
+                                              const T* __restrict__ v_lds, int b, int h, int qi, int col, int g,
+                                              float& off, const Issue& issue, PendingOut<T>& pend) {
+    static_assert(!kDefer || (kVec && D == 16), "deferred stores: vector IO, head dim 16");
     typedef typename Frag<T>::x4 X4;
     typedef typename Frag<T>::x8 X8;
     constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
@@ -1087,12 +1179,10 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
 
     static_assert(D == 16 || !kRec, "head dim 32: one head per workgroup");
     // Q^T operand of S^T = K Q^T (16x16x32): lane (col, g) holds elements
-    // 8g..8g+7 of query col's LDS row, i.e. Q_hi dims for g < 2 and Q_lo
-    // dims for g >= 2 (head dim 16); head dim 32: Q_hi dims 8g..8g+7 (qf)
-    // and Q_lo dims 8g..8g+7 (qf_lo), two products per score tile.
-    const X8 qf = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * (2 * D) + 8 * g]);
-    X8 qf_lo = qf;
-    if constexpr (D == 32) qf_lo = *reinterpret_cast<const X8*>(&q_lds[(wave * 16 + col) * 64 + 32 + 8 * g]);
+    // 8g..8g+7 of the k-slices of query col, i.e. Q_hi (g even) or Q_lo
+    // (g odd) of dims 8(g >> 1) .. + 7 (head dim 16, store_q4, q_operand);
+    // head dim 32: Q_hi dims 8g..8g+7 (qf) and Q_lo dims 8g..8g+7 (qf_lo),
+    // two products per score tile.
     // S^T of one tile from its K fragment and accumulator input
     auto score = [&](const X8& kfr, const f32x4& c) -> f32x4 {
         const f32x4 s = Frag<T>::mma32(kfr, qf, c);
@@ -1102,13 +1192,18 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             return s;
     };
 
-    // K operand: lane (col, g) reads row col of the tile, dims 8(g&1)..+7
+    // K operand: lane (col, g) reads row col of the tile, dims 8(g>>1)..+7
     // (head dim 16; kRec: k_lds and v_lds point at this head's row in the
-    // first record) or dims 8g..+7 (head dim 32)
+    // first record) or dims 8g..+7 (head dim 32).  At head dim 16 lanes
+    // 0-31 read the first 16 bytes of the 16 rows and lanes 32-63 the
+    // second: a 16-byte LDS read serves lanes 0-31 in one pass, and with
+    // lanes 16-31 on the second half of the same rows (dims 8(g&1)) the
+    // 208-byte records had put two lanes on one bank (measured: 8.3 against
+    // 4.5 cycles per read).
     constexpr int kKTile = kRec ? 16 * kKRec : 16 * D;  // elements from one K tile to the next
     constexpr int kVTile = kRec ? 16 * kVRec : 16 * D;
-    const T* kbase = kRec ? k_lds + col * kKRec + (g & 1) * 8
-                          : k_lds + (D == 32 ? g : (g & 1)) * 128 + col * 8;
+    const T* kbase = kRec ? k_lds + col * kKRec + (g >> 1) * 8
+                          : k_lds + (D == 32 ? g : (g >> 1)) * 128 + col * 8;
     auto kfrag = [&](int t) -> X8 { return *reinterpret_cast<const X8*>(kbase + t * kKTile); };
     // V^T fragments by transpose reads of row-major V (lds_read_tr); head
     // dim 32 reads dims 16..31 at vrow + 16 for the second half of O
@@ -1252,6 +1347,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
 #pragma unroll
         for (int pr = 0; pr < kPairs; ++pr) {
             __builtin_amdgcn_sched_barrier(0);
+            if ((pr * 4) % kPairs < 4) set_wave_prio(3 - (pr * 4) / kPairs);  // at each quarter
             // the next window's DMA rounds ceil(pr R / P) .. ceil((pr+1) R / P) - 1
 #pragma unroll
             for (int k = (pr * Issue::kRounds + kPairs - 1) / kPairs;
@@ -1292,6 +1388,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         }
         __builtin_amdgcn_sched_barrier(0);
     }
+    set_wave_prio(0);
 
     float l = lacc[0];  // every row of ones^T P^T holds the sum of query col
     const bool bad = qi < N && !(l >= kRowSumMin && l <= kRowSumMax);  // also NaN and inf
@@ -1363,7 +1460,11 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     }
 
     // lane holds O[qi][4g + r], r = 0..3 (head dim 32: and O[qi][16 + 4g + r])
-    if (qi < N) {
+    if constexpr (kDefer) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pend.r[r] = T(o[r] * inv);
+    } else if (qi < N) {
         T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
         const float inv = 1.0f / l;
         X4 res;
@@ -1594,8 +1695,15 @@ swin_attention_tuned_kernel(const Params p) {
     constexpr int kStageWaves = kGroupSlots ? kWaves * HPW : kWaves;  // waves sharing a window's DMA
     static_assert(!kGroupSlots || waves_per_eu<T, NT, kMask, kVec>() * 4 >= kWaves * HPW,
                   "the strip groups' waves must fit one CU's SIMDs together");
-    // Q rows are wave-private on the LDS-DMA path (a wave stores and reads
-    // only its own 16 rows, in that order), so one buffer serves there.
+    // 2-byte LDS-DMA staging: K and V in DMA rounds (all at once for the
+    // first window and for waves without a strip, spread over the compute of
+    // the previous window otherwise); Q by register
+    constexpr bool kSpread = kVec && v_row_major<T>();  // Stage<T, NT, true>::kDma
+    // head dim 16 on that path keeps Q in registers (load_qraw, q_operand);
+    // head dim 32 passes it through LDS, whose rows are wave-private there (a
+    // wave stores and reads only its own 16 rows, in that order), so one
+    // buffer serves
+    constexpr bool kQReg = kSpread && D == 16;
     constexpr int kQBufs = HPW > 1 || kSingle ? 1 : 2;
     constexpr int kKVBufs = kSingle ? 1 : 2;
     static_assert(HPW == 1 || (kVec && v_row_major<T>()), "several heads per workgroup need the LDS-DMA path");
@@ -1604,7 +1712,7 @@ swin_attention_tuned_kernel(const Params p) {
     // lands in its padding)
     constexpr int kKLds = kRecs ? rec_loads(NT) * 512 : St::kRows * D;
     constexpr int kVLdsAll = kRecs ? 8 : St::kVLds;
-    __shared__ __attribute__((aligned(16))) T q_lds[kQBufs][HPW][St::kQRows * q_row_len<T, D>()];
+    __shared__ __attribute__((aligned(16))) T q_lds[kQBufs][HPW][kQReg ? 8 : St::kQRows * q_row_len<T, D>()];
     __shared__ __attribute__((aligned(16))) T k_lds[kKVBufs][kKLds];
     __shared__ __attribute__((aligned(16))) T vt_lds[kKVBufs][kVLdsAll];
     __shared__ __attribute__((aligned(4))) uint8_t cls_lds[kMask == kMaskRegion ? NP : 4];
@@ -1636,7 +1744,11 @@ swin_attention_tuned_kernel(const Params p) {
     const int i1 = kStrided ? (p.B - range + p.ranges - 1) / p.ranges : min(p.B, i0 + p.win_per_wg);
 
     const int lane = threadIdx.x & 63;
-    const int wave = HPW > 1 ? (threadIdx.x >> 6) & (kWaves - 1) : threadIdx.x >> 6;  // strip within the group
+    // wave-uniform, and provably so (scalar registers): the strip index, and
+    // with it `active`, then steer branches the compiler keeps scalar, and
+    // values assigned under them stay in scalar registers
+    const int wave_id = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+    const int wave = HPW > 1 ? wave_id & (kWaves - 1) : wave_id;  // strip within the group
     const int col = lane & 15;
     const int g = lane >> 4;
     const int strip = grp * kWaves + wave;
@@ -1665,6 +1777,108 @@ swin_attention_tuned_kernel(const Params p) {
     const float qscale = sizeof(T) == 2 ? p.scale * kLog2e : p.scale;
     float off = 0.0f;  // row offset of the offset softmax (2-byte types, log2 units)
 
+    // records: the lane's load offsets per round, the same for every window
+    int rec_off[kRecs ? kRecRounds<St, kRecs>() : 1];
+    if constexpr (kRecs) {
+#pragma unroll
+        for (int r = 0; r < kRecRounds<St, kRecs>(); ++r) rec_off[r] = St::rec_voff(p, r);
+    }
+    typedef typename Frag<T>::x8 X8;
+    constexpr bool kTensor = mask_tensor(kMask);
+
+    if constexpr (kQReg) {
+        // Head dim 16 on the LDS-DMA path: while window i is computed, its DMA
+        // rounds bring in window i + 1's K and V, and Q travels by register
+        // (load_qraw at the window top, q_operand after the end-of-window
+        // wait).  A window's output is stored at the next window's top
+        // (PendingOut).
+        // the window being computed (b0, code0, flag0: tensor mode reads its
+        // mask) and the next one (b1, ...), as plain scalars: a struct here
+        // was kept in memory, which the compiler placed in LDS
+        typedef typename St::WindowDesc WD;
+        WindowIter<kMask> it;
+        it.init(p, i0);
+        if constexpr (kStrided) {
+            it.base = range;
+            it.stride = p.ranges;
+        }
+        auto window_flag = [&](int bw) {
+            if constexpr (kTensor) return p.boundary == nullptr || p.boundary[bw] != 0;
+            return true;
+        };
+        int code0;
+        int b0 = it.window(p, code0);
+        bool flag0 = window_flag(b0);
+        QRaw<T> qraw;
+        X8 qf = {};
+        {
+            const WD d0 = St::template window_desc<kRecs>(p, b0, h, h0);
+#pragma unroll
+            for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r)
+                St::template dma_round<kRecs>(p, d0, k_lds[0], vt_lds[0], r, kRecs ? rec_off[r] : 0);
+        }
+        if (active) qraw = load_qraw<T>(p, b0, h, qi, g);
+        wait_vmem();
+        if (active) qf = q_operand<T>(qraw, qscale, g);
+        __syncthreads();  // the first window's rows and the region classes
+
+        f32x4 bs[NT];
+        PendingOut<T> pend;
+        int b_out = -1;  // the window whose output pend holds, or -1 (wave-uniform)
+        int code_cur = -1;
+        bool rebuild = false;  // this wave's offsets moved: rebuild its tiles (wave-uniform)
+        for (int i = i0; i < i1; ++i) {
+            const int buf = (i - i0) & 1;
+            const bool more = i + 1 < i1;
+            // New bias (+ region mask) tiles are built before the next
+            // window's rows are requested: the vector-memory counter retires
+            // in order, so waiting for the bias loads after that request
+            // would wait for the rows as well.
+            if (active && (code0 != code_cur || rebuild)) {  // code is workgroup-uniform
+                build_tiles<NT, kMask, true>(bs, p, h, qi, g, code0, cls_lds, off);
+                code_cur = code0;
+                rebuild = false;
+            }
+            if (b_out >= 0) {
+                store_out4<T>(p, pend.r, b_out, h, qi, g);
+                b_out = -1;
+            }
+            int b1 = b0, code1 = code0;
+            bool flag1 = flag0;
+            WD d1 = {};
+            if (more) {
+                it.next(p);
+                b1 = it.window(p, code1);
+                flag1 = window_flag(b1);
+                d1 = St::template window_desc<kRecs>(p, b1, h, h0);
+                if (active) qraw = load_qraw<T>(p, b1, h, qi, g);
+            }
+            const DmaIssuer<T, St, kRecs, kStageWaves> issue{&p, d1, k_lds[buf ^ 1], vt_lds[buf ^ 1], rec_off, more};
+            T* const kw = k_lds[buf] + (kRecs ? 16 * slot : 0);  // this head's rows of each record
+            T* const vw = kRecs ? k_lds[buf] + kRecV + 16 * slot : vt_lds[buf];
+            if (active) {
+                if (kTensor && flag0)
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, D, true>(
+                        p, bs, qf, qf, kw, vw, b0, h, qi, col, g, off, issue, pend);
+                else
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, D, true>(
+                        p, bs, qf, qf, kw, vw, b0, h, qi, col, g, off, issue, pend);
+                b_out = b0;
+            } else {
+#pragma unroll
+                for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r) issue(r);
+            }
+            wait_vmem();  // this wave's DMA rows (and its Q) have landed
+            if (active && more) qf = q_operand<T>(qraw, qscale, g);
+            __syncthreads();
+            b0 = b1;
+            code0 = code1;
+            flag0 = flag1;
+        }
+        if (b_out >= 0) store_out4<T>(p, pend.r, b_out, h, qi, g);
+        return;
+    }
+
     St st;
     WindowIter<kMask> it;
     it.init(p, i0);
@@ -1681,16 +1895,6 @@ swin_attention_tuned_kernel(const Params p) {
     bool flag_next = true;
     if constexpr (kMask != kNoMask && kMask != kMaskRegion)
         flag_next = p.boundary == nullptr || p.boundary[b_next] != 0;
-    // 2-byte LDS-DMA staging: the Q rows by register, K and V in DMA rounds
-    // (all at once here and for waves without a strip, spread over the
-    // compute of the previous window otherwise)
-    constexpr bool kSpread = kVec && v_row_major<T>();  // Stage<T, NT, true>::kDma
-    // records: the lane's load offsets per round, the same for every window
-    int rec_off[kRecs ? kRecRounds<St, kRecs>() : 1];
-    if constexpr (kRecs) {
-#pragma unroll
-        for (int r = 0; r < kRecRounds<St, kRecs>(); ++r) rec_off[r] = St::rec_voff(p, r);
-    }
     auto stage_load = [&](int bw, int sb) {
         if constexpr (kSpread) {
             st.load_q(p, bw, h, q0);
@@ -1709,6 +1913,7 @@ swin_attention_tuned_kernel(const Params p) {
     __syncthreads();
 
     f32x4 bs[NT];
+    PendingOut<T> pend;  // unused: these paths store each strip's output at once
     for (int i = i0; i < i1; ++i) {
         const int buf = kKVBufs == 2 ? (i - i0) & 1 : 0;
         const int nbuf = kKVBufs == 2 ? buf ^ 1 : 0;  // the next window's K/V buffer
@@ -1751,16 +1956,19 @@ swin_attention_tuned_kernel(const Params p) {
         T* const kw = k_lds[buf] + (kRecs ? 16 * slot : 0);  // this head's rows of each record
         T* const vw = kRecs ? k_lds[buf] + kRecV + 16 * slot : vt_lds[buf];
         if (active) {
-            constexpr bool kTensor = kMask != kNoMask && kMask != kMaskRegion;
             bool use_mask = false;
             if constexpr (kTensor) use_mask = flag;
             if constexpr (sizeof(T) == 2) {
+                // Q operands from the wave's LDS rows
+                const X8 qa = *reinterpret_cast<const X8*>(&qw[(wave * 16 + col) * (2 * D) + 8 * g]);
+                X8 qb = qa;
+                if constexpr (D == 32) qb = *reinterpret_cast<const X8*>(&qw[(wave * 16 + col) * 64 + 32 + 8 * g]);
                 if (use_mask)
-                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, D, Issuer>(
-                        p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
+                    rebuild = attend_offset<T, NT, kMask, kTensor, kVec, kRecs, D, false, Issuer>(
+                        p, bs, qa, qb, kw, vw, b, h, qi, col, g, off, issue, pend);
                 else
-                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, D, Issuer>(
-                        p, bs, qw, kw, vw, b, h, wave, qi, col, g, off, issue);
+                    rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, D, false, Issuer>(
+                        p, bs, qa, qb, kw, vw, b, h, qi, col, g, off, issue, pend);
             } else {
                 if (use_mask)
                     attend_f32<T, NT, kMask, kTensor, kVec>(p, bs, qw, kw, vw, b, h, wave, qi, col, g);
