@@ -261,6 +261,38 @@ def bench_attention(args, dev):
     t_shift = _steady_time(attn_shifted, args.warmup, args.steps, dev)
     res = dict(t_attn=t_attn, t_shift=t_shift)
 
+    # The layout the reference's own patch hands the kernel
+    # (torch-ext/crumpet/monai_patch.py:167-191): the mask repeated over the
+    # outer batch to [1372, 343, 343] and one flag per window from
+    # abs().amax over its mask; window b then reads mask row block b.  Timed
+    # as the kernel alone (mask and flags built once) and as the patch's
+    # whole per-call sequence (repeat, flags, attention).
+    from crumpet_amd.fused_attention import fused_swin_attention
+
+    mask_rep = mask.repeat(B // mask.shape[0], 1, 1)
+    bnd_rep = (mask_rep.abs().amax(dim=(1, 2)) > 0).to(torch.uint8)
+
+    def attn_rep(i):
+        t = views[i % R]
+        fused_swin_attention(t[0], t[1], t[2], bias, mask_rep, bnd_rep, 0.25, out=ovs[i % R])
+
+    def attn_rep_call(i):
+        t = views[i % R]
+        m = mask.repeat(B // mask.shape[0], 1, 1)
+        fl = (m.abs().amax(dim=(1, 2)) > 0).to(torch.uint8)
+        fused_swin_attention(t[0], t[1], t[2], bias, m, fl, 0.25, out=ovs[i % R])
+
+    res["t_attn_rep"] = _steady_time(attn_rep, args.warmup, args.steps, dev)
+    res["t_attn_rep_call"] = _steady_time(attn_rep_call, args.warmup, max(10, args.steps // 2), dev)
+    attn_rep(0)
+    torch.cuda.synchronize()
+    rep_out = ovs[0].clone()
+    attn(0)
+    torch.cuda.synchronize()
+    res["rep_equals_343_form"] = bool(torch.equal(rep_out, ovs[0]))
+    del mask_rep, bnd_rep, rep_out
+    torch.cuda.empty_cache()
+
     # accuracy on a sample of windows vs fp32 torch (GPU) of the same inputs
     t = views[0]
     attn(0)
@@ -365,9 +397,15 @@ STAGES = [  # config 4: (name, padded dim, C, heads, window, shift)
 def bench_blocks(args, dev):
     """Config 4: partition -> fused attention -> unpartition per Swin stage, B=4.
 
-    The windows' C channels are read as H heads of 16 (q = k = v = the
-    partitioned tokens, so the timed chain is exactly the three hot-path
-    kernels; the qkv/proj linears are library GEMMs outside the path)."""
+    The windows' C channels are read as H heads of 16.  q is the freshly
+    partitioned tokens; k and v are the same tokens with the heads rotated
+    by one and two (the workload tests/test_gpu_block_path.py checks:
+    independent of q, as a qkv projection makes them), held in buffers made
+    once before timing, so the timed chain is exactly the three hot-path
+    kernels (the qkv/proj linears are library GEMMs outside the path).
+    ``ms_qkv_equal`` times the same chain with k = v = q: every row's
+    diagonal score is then 0.25 |q|^2, and in fp16 the rows whose diagonal
+    passes 2^16 take the offset softmax's exact pass."""
     import torch
 
     import crumpet_amd
@@ -390,16 +428,26 @@ def bench_blocks(args, dev):
             rpi = torch.from_numpy((rel[0] * (2 * ws[1] - 1) + rel[1]) * (2 * ws[2] - 1) + rel[2])
             bias = table[rpi.reshape(-1)].reshape(N, N, H).permute(2, 0, 1).contiguous().to(dtype).to(dev)
 
-            def step(i):
-                w = crumpet_amd.fused_shift_partition_3d(x, ws, ss)
-                nwin = w.shape[0]
-                t = w.view(nwin, N, H, 16).permute(0, 2, 1, 3)
-                o = torch.empty_like(w)
-                fused_swin_attention_shifted(t, t, t, bias, (dim,) * 3, ws, ss, 0.25,
-                                             o.view(nwin, N, H, 16).permute(0, 2, 1, 3))
-                crumpet_amd.fused_unshift_unpartition_3d(o, B, dim, dim, dim, C, ws, ss)
+            w0 = crumpet_amd.fused_shift_partition_3d(x, ws, ss)
+            t0 = w0.view(w0.shape[0], N, H, 16).permute(0, 2, 1, 3)
+            tk = torch.roll(t0, 1, dims=1)  # heads rotated by one and two
+            tv = torch.roll(t0, 2, dims=1)
+            del w0, t0
 
+            def chain(rotated):
+                def step(i):
+                    w = crumpet_amd.fused_shift_partition_3d(x, ws, ss)
+                    nwin = w.shape[0]
+                    t = w.view(nwin, N, H, 16).permute(0, 2, 1, 3)
+                    o = torch.empty_like(w)
+                    fused_swin_attention_shifted(t, tk if rotated else t, tv if rotated else t, bias, (dim,) * 3,
+                                                 ws, ss, 0.25, o.view(nwin, N, H, 16).permute(0, 2, 1, 3))
+                    crumpet_amd.fused_unshift_unpartition_3d(o, B, dim, dim, dim, C, ws, ss)
+                return step
+
+            step = chain(True)
             ms = _steady_time(step, args.warmup, args.steps, dev)
+            ms_equal = _steady_time(chain(False), args.warmup, args.steps, dev)
             # the same three launches replayed as one HIP graph (no host launch overhead)
             cap = torch.cuda.Stream()
             cap.wait_stream(torch.cuda.current_stream())
@@ -415,7 +463,9 @@ def bench_blocks(args, dev):
             tokens = B * dim ** 3
             part_bytes = 2 * tokens * C * x.element_size()
             flops = 4 * N * N * 16 * H * (tokens // N)
+            del tk, tv
             res[f"{name}_{tag}"] = {"ms": round(ms, 5), "ms_graph_replay": round(ms_graph, 5),
+                                    "ms_qkv_equal": round(ms_equal, 5),
                                     "shape": [B, dim, dim, dim, C], "heads": H,
                                     "window": list(ws), "shift": list(ss),
                                     "partition_bytes": part_bytes, "attention_flops": flops,
@@ -935,6 +985,14 @@ def main():
         if "t_eager" in a:
             comp["eager_rocm_ms"] = round(a["t_eager"], 4)
             comp["speedup_vs_eager"] = round(a["t_eager"] / a["t_attn"], 2)
+        comp["mask_1372_form"] = {
+            "ms": round(a["t_attn_rep"], 5),
+            "ms_with_repeat_and_flags": round(a["t_attn_rep_call"], 5),
+            "frac_hbm": round(C3_BYTES / (a["t_attn_rep"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "same_output_as_343_form": a["rep_equals_343_form"],
+            "workload": "the reference patch's layout (monai_patch.py:167-191): mask.repeat to "
+                        "[1372,343,343] + abs().amax boundary flags; 'with_repeat_and_flags' times the "
+                        "patch's per-call sequence"}
         components["attention"] = comp
         tfl_s = C3_FLOPS / (a["t_shift"] * 1e-3) / 1e12
         comp_s = {"ms": round(a["t_shift"], 5), "TFLOP_s": round(tfl_s, 2),

@@ -105,11 +105,16 @@ def window_proj_3d(
     return out
 
 
+def _linear(m):
+    """(weight, bias) of a Linear module, or the pair itself."""
+    return (m.weight, m.bias) if isinstance(m, torch.nn.Linear) else tuple(m)
+
+
 def fused_window_msa_3d(
     x: torch.Tensor,  # [B, D, H, W, C] block input (before norm1)
     norm: torch.nn.LayerNorm,
-    qkv: torch.nn.Linear,
-    proj: torch.nn.Linear,
+    qkv,  # torch.nn.Linear, or its (weight, bias)
+    proj,  # torch.nn.Linear, or its (weight, bias)
     relative_position_bias: torch.Tensor,  # [heads, N, N]
     num_heads: int,
     scale: float,
@@ -123,7 +128,9 @@ def fused_window_msa_3d(
 
     With a non-zero shift the shifted-window mask is derived from the padded
     volume's geometry (``region=True``, nothing is read) or taken from
-    ``mask`` (``[nW, N, N]``, window b reads ``mask[b mod nW]``).
+    ``mask`` (``[nW, N, N]``, window b reads ``mask[b mod nW]``).  ``qkv`` and
+    ``proj`` are Linear modules or ``(weight, bias)`` pairs; weights already
+    in ``dtype`` and contiguous are used as they are (no cast kernel).
     """
     ws = as_triple("window_size", window_size, signed=True)
     ss = as_triple("shift_size", shift_size, signed=True)
@@ -132,7 +139,9 @@ def fused_window_msa_3d(
     hd = C // num_heads
     padded = padded_dims((D, H, W), ws)
     n = ws[0] * ws[1] * ws[2]
-    qkv_out = window_qkv_3d(x, qkv.weight, qkv.bias, ws, ss, norm.weight, norm.bias, norm.eps, True, dtype)
+    wq, bq = _linear(qkv)
+    wp, bp = _linear(proj)
+    qkv_out = window_qkv_3d(x, wq, bq, ws, ss, norm.weight, norm.bias, norm.eps, True, dtype)
     nwin = qkv_out.shape[0]
     t = qkv_out.view(nwin, n, 3, num_heads, hd).permute(2, 0, 3, 1, 4)
     attn = torch.empty((nwin, n, num_heads, hd), dtype=dtype, device=x.device)
@@ -146,4 +155,4 @@ def fused_window_msa_3d(
                                      flags.repeat(nwin // nw).contiguous(), scale, ov)
     else:
         fused_swin_attention_windows(t[0], t[1], t[2], relative_position_bias, None, None, scale, ov)
-    return window_proj_3d(attn.view(nwin, n, C), proj.weight, proj.bias, B, D, H, W, ws, ss)
+    return window_proj_3d(attn.view(nwin, n, C), wp, bp, B, D, H, W, ws, ss)

@@ -140,10 +140,53 @@ def _fused_block_supported(block, x: torch.Tensor) -> bool:
     return c % 16 == 0 and c <= 384 and _fits_staging_tile(c, _ESIZE[_compute_dtype(x)])
 
 
+def _cached(module, key, sources, make):
+    """``make()`` for ``key``, kept on ``module`` until a tensor in ``sources``
+    changes: an in-place update bumps its version counter, reassigning it
+    changes its storage.  Under graph capture nothing is cached or reused:
+    the value is recomputed by kernels the graph records, so every replay
+    reads the parameters as they are then (the reference recomputes the bias
+    on every call for that reason, torch-ext/crumpet/monai_patch.py:157-162)."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        return make()
+    stamp = tuple((t._version, t.data_ptr()) for t in sources)
+    cache = module.__dict__.setdefault("_crumpet_cache", {})
+    hit = cache.get(key)
+    if hit is not None and hit[0] == stamp:
+        return hit[1]
+    with torch.no_grad():
+        value = make()
+    cache[key] = (stamp, value)
+    return value
+
+
+def _window_bias(attn, n):
+    """``[heads, n, n]`` relative-position bias of the first ``n`` window
+    tokens, gathered from the transposed table (unit stride along keys) and
+    kept in the table's dtype; cached on the module (``_cached``)."""
+    def make():
+        idx = attn.relative_position_index[:n, :n].reshape(-1)
+        return attn.relative_position_bias_table.t()[:, idx].view(attn.num_heads, n, n)
+
+    return _cached(attn, ("bias", n), (attn.relative_position_bias_table, attn.relative_position_index), make)
+
+
+def _cast_linear(lin, dtype):
+    """``(weight, bias)`` of a Linear in ``dtype``, contiguous, as autocast
+    casts them for the forward; cached on the module (``_cached``)."""
+    def make():
+        return (lin.weight.to(dtype).contiguous(),
+                lin.bias.to(dtype).contiguous() if lin.bias is not None else None)
+
+    sources = (lin.weight,) if lin.bias is None else (lin.weight, lin.bias)
+    return _cached(lin, ("cast", dtype), sources, make)
+
+
 def _fused_block_forward(block, x, mask_matrix, swin):
     """forward_part1 as three kernels: window_qkv_3d (norm1, pad, shift,
     partition, qkv), the fused attention, window_proj_3d (proj, reverse,
-    unshift, crop)."""
+    unshift, crop).  The gathered bias and the cast projection weights are
+    cached per module, so a call launches just the three kernels."""
     b, d, h, w, c = x.shape
     window_size, shift_size = swin.get_window_size((d, h, w), block.window_size, block.shift_size)
     ws = _as_triple(window_size)
@@ -151,12 +194,13 @@ def _fused_block_forward(block, x, mask_matrix, swin):
     padded = tuple(-(-n // k) * k for n, k in zip((d, h, w), ws))
     attn = block.attn
     n = ws[0] * ws[1] * ws[2]
-    idx = attn.relative_position_index[:n, :n].reshape(-1)
-    bias = attn.relative_position_bias_table.t()[:, idx].view(attn.num_heads, n, n)
+    dtype = _compute_dtype(x)
+    bias = _window_bias(attn, n)
     shifted = any(s > 0 for s in ss)
     region = shifted and getattr(mask_matrix, _GEOMETRY_ATTR, None) == (*padded, ws, ss)
-    return fused_window_msa_3d(x, block.norm1, attn.qkv, attn.proj, bias, attn.num_heads, attn.scale, ws, ss,
-                               mask=mask_matrix if shifted else None, region=region, dtype=_compute_dtype(x))
+    return fused_window_msa_3d(x, block.norm1, _cast_linear(attn.qkv, dtype), _cast_linear(attn.proj, dtype),
+                               bias, attn.num_heads, attn.scale, ws, ss,
+                               mask=mask_matrix if shifted else None, region=region, dtype=dtype)
 
 
 def _patched_forward_part1(original, swin):
@@ -212,9 +256,7 @@ def _patched_window_attention_forward(original):
 
         qkv = self.qkv(x)  # [b, n, 3c]; channel = s*c + h*hd + d
         t = qkv.view(b, n, 3, heads, hd).permute(2, 0, 3, 1, 4)  # views [b, H, n, hd]
-        idx = self.relative_position_index[:n, :n].reshape(-1)
-        # gather from the transposed table: [H, n*n], unit stride along keys
-        bias = self.relative_position_bias_table.t()[:, idx].view(heads, n, n)
+        bias = _window_bias(self, n)
         out = torch.empty((b, n, heads, hd), dtype=qkv.dtype, device=qkv.device)
         ov = out.permute(0, 2, 1, 3)
         region = getattr(self, _REGION_ATTR, None)

@@ -98,3 +98,37 @@ def test_compat_feature48_parameter_count():
     # MONAI's SwinUNETR(feature_size=48, depths (2,2,2,2), heads (3,6,12,24), out 14) has 62.19 M parameters
     m = sw.SwinUNETR(in_channels=1, out_channels=14, feature_size=48)
     assert sum(p.numel() for p in m.parameters()) == 62_187_296
+
+
+def test_module_cache_follows_parameter_updates():
+    """The fused block's cached bias gather and weight casts are recomputed
+    when a source tensor changes in place (version counter) or is replaced
+    (storage), and reused otherwise."""
+    import torch
+
+    from crumpet_amd import monai_patch
+    from crumpet_amd.swin_unetr_compat import WindowAttention
+
+    torch.manual_seed(3)
+    attn = WindowAttention(dim=48, num_heads=3, window_size=(7, 7, 7), qkv_bias=True)
+    first = monai_patch._window_bias(attn, 343)
+    assert first.shape == (3, 343, 343)
+    assert monai_patch._window_bias(attn, 343) is first
+    idx = attn.relative_position_index[:343, :343].reshape(-1)
+    assert torch.equal(first, attn.relative_position_bias_table.t()[:, idx].view(3, 343, 343))
+    with torch.no_grad():
+        attn.relative_position_bias_table.add_(1.0)  # in place: version bump
+    second = monai_patch._window_bias(attn, 343)
+    assert second is not first and torch.equal(second, first + 1.0)
+    # a smaller window (the 6^3 stage rule) is a separate entry
+    assert monai_patch._window_bias(attn, 216).shape == (3, 216, 216)
+
+    w, b = monai_patch._cast_linear(attn.qkv, torch.float16)
+    assert w.dtype == torch.float16 and w.is_contiguous() and torch.equal(w, attn.qkv.weight.half())
+    assert monai_patch._cast_linear(attn.qkv, torch.float16)[0] is w
+    attn.qkv.weight = torch.nn.Parameter(torch.zeros_like(attn.qkv.weight))  # replaced: new storage
+    w2, _ = monai_patch._cast_linear(attn.qkv, torch.float16)
+    assert w2 is not w and not w2.any()
+    # the compute dtype equal to the parameters' returns them as they are
+    w3, b3 = monai_patch._cast_linear(attn.proj, torch.float32)
+    assert w3 is attn.proj.weight and b3 is attn.proj.bias
