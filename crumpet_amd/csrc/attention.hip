@@ -59,7 +59,12 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     if (Dh != 16 && Dh != 32 && Dh != 64 && Dh != 128)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: head_dim %lld is not supported (16, 32, 64 or 128)",
                     what, (long long)Dh);
-    const bool wide = Dh != 16 || N > 512;
+    // The tuned kernel feeds q * scale * log2(e) to the score product (its
+    // scores come out in log2 units).  An fp16 q is at most 65504, so that
+    // product can overflow fp16 only for |scale| > ln 2; such calls run the
+    // general kernel, which rounds q * scale as the reference does.
+    const bool fold_log2e = !(dtype == CRUMPET_DTYPE_F16 && fabsf(scale) > 0.6931472f);
+    const bool wide = Dh != 16 || N > 512 || !fold_log2e;
     if (wide && N > 0x3fffffffLL)
         return fail(CRUMPET_ERR_UNSUPPORTED, "%s: N = %lld is too large", what, (long long)N);
     if (wide && region != nullptr && N > attn::kWideMaxRegionN)
@@ -206,7 +211,7 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                                                          : attn::kMaskF16;
     // head dim 32 runs the tuned kernel for 2-byte types with vector IO at
     // 14 or 22 tiles (129 <= N <= 352), addressed with 32-bit byte offsets
-    bool tuned32 = Dh == 32 && dtype != CRUMPET_DTYPE_F32 && vec && N <= 512 &&
+    bool tuned32 = Dh == 32 && dtype != CRUMPET_DTYPE_F32 && vec && N <= 512 && fold_log2e &&
                    attn::d32_tiles(attn::select_tiles(N));
     for (int i = 0; i < 3; ++i) {
         if (((N - 1) * st[i][2] + 32) * esize >= (int64_t(1) << 31)) tuned32 = false;

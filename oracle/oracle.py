@@ -330,6 +330,44 @@ def attention(q, k, v, bias, mask=None, boundary=None, scale=None, dtype=np.floa
     return out
 
 
+def attention_reference_numerics(q, k, v, bias, mask=None, scale=None, block_n: int = 32):
+    """The attention formula with the rounding steps of the reference's Triton
+    kernel (torch-ext/crumpet/fused_attention.py:82-146), for 2-byte inputs:
+    q * scale computed in fp32 and rounded to the input dtype (:88); scores
+    and bias + mask in fp32 (:109-128); an online softmax over ``block_n``-key
+    chunks (:133-140) whose P is rounded to the input dtype before P V, with
+    the row sum taken over the unrounded fp32 P and the accumulator rescaled
+    in fp32; the result rounded to the input dtype (:142-148).
+
+    q, k, v: torch tensors [B, H, N, D] (float16 / bfloat16 / float32, CPU);
+    bias [H, N, N]; mask [B, N, N] (already tiled per window) or None.
+    Returns a torch tensor of q's dtype.  Used to bound what the input
+    dtype's rounding alone costs against the exact formula (``attention``).
+    """
+    import torch
+
+    dt = q.dtype
+    B, H, N, D = q.shape
+    if scale is None:
+        scale = D ** -0.5
+    qs = (q.float() * scale).to(dt).float()
+    m = torch.full((B, H, N), -float("inf"))
+    l = torch.zeros((B, H, N))
+    acc = torch.zeros((B, H, N, D))
+    for n0 in range(0, N, block_n):
+        n1 = min(N, n0 + block_n)
+        s = qs @ k[:, :, n0:n1].float().transpose(-1, -2) + bias[None, :, :, n0:n1].float()
+        if mask is not None:
+            s = s + mask[:, None, :, n0:n1].float()
+        m_new = torch.maximum(m, s.amax(-1))
+        alpha = torch.exp(m - m_new)
+        p = torch.exp(s - m_new[..., None])
+        l = l * alpha + p.sum(-1)
+        acc = acc * alpha[..., None] + p.to(dt).float() @ v[:, :, n0:n1].float()
+        m = m_new
+    return (acc / l[..., None]).to(dt)
+
+
 # --------------------------------------------------------------------------
 # fused window-MSA block projections (the chain around the attention)
 # --------------------------------------------------------------------------

@@ -152,6 +152,56 @@ def test_shifted_regions_general_kernel(oracle, dev, Dh, dtype):
     _compare(out, ref, dtype, f"region Dh={Dh} N={N} {dtype}")
 
 
+@pytest.mark.parametrize("Dh", [64, 128])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_shifted_regions_scale_quarter_rounding_limit(oracle, dev, Dh, dtype):
+    """The region case above at scale 0.25 for head dims 64 and 128, where
+    scores spread widely.  There the input type's rounding of P alone moves
+    the result: the reference kernel's own numerics (oracle
+    attention_reference_numerics: q*scale rounded, P rounded before P V,
+    fp32 row sums) land 1.23e-2 from the fp32 formula at head dim 128 in
+    bf16, above the 1e-2 tolerance.  The tolerance of each case is therefore
+    the larger of the dtype's and 1.25 x the reference numerics' own error on
+    the same inputs: the kernel must be as close to the formula as the
+    reference's arithmetic is."""
+    vol, ws, ss = (14, 14, 14), (7, 7, 7), (3, 3, 3)
+    nW, N = 8, 343
+    B, H = nW * 2, 2
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3400 + N)
+    bias = bias_from_table(trunc_normal_table(13 ** 3, H, 3401 + N), ws).to(dtype)
+    m = oracle.attn_mask(*vol, ws, ss, "float32")
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m, None, scale=0.25)
+    mt = torch.from_numpy(m)[torch.arange(B) % nW]
+    refnum = oracle.attention_reference_numerics(q, k, v, bias, mt, scale=0.25)
+    limit = float(np.abs(refnum.float().numpy() - ref).max())
+    tol = max(TOL[dtype], 1.25 * limit)
+    out = fused_swin_attention_shifted(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), vol, ws, ss, scale=0.25)
+    got = out.float().cpu().numpy()
+    err = float(np.abs(got - ref).max())
+    print(f"region Dh={Dh} scale 0.25 {dtype}: max-abs {err:.3e}, reference numerics {limit:.3e}, "
+          f"tol {tol:.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err <= tol
+
+
+@pytest.mark.parametrize("Dh", [16, 32])
+def test_fp16_scale_above_ln2_with_large_q(oracle, dev, Dh):
+    """fp16 with scale 1.0 and |q| up to about 4e4: q * scale * log2(e), the
+    operand the tuned kernel builds, would overflow fp16 (q * scale itself
+    does not), so such calls run the general kernel, which rounds q * scale
+    as the reference does.  Checked against the fp32 formula at N = 343."""
+    dtype = torch.float16
+    B, H, N = 4, 3, 343
+    q = (seeded((B, H, N, Dh), torch.float32, 3600 + Dh) * 1e4).clamp(-6e4, 6e4).to(dtype)
+    k = (seeded((B, H, N, Dh), torch.float32, 3601 + Dh) * 1e-4).to(dtype)
+    v = seeded((B, H, N, Dh), dtype, 3602 + Dh)
+    assert float(q.float().abs().max()) * 1.4426950408889634 > 65504
+    bias = bias_from_table(trunc_normal_table(2197, H, 3603 + Dh), (7, 7, 7)).to(dtype)
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), None, None, scale=1.0)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), None, scale=1.0)
+    _compare(out, ref, dtype, f"fp16 scale 1.0, large q, Dh={Dh}")
+
+
 @pytest.mark.parametrize("N", [513, 729, 1000])
 def test_head_dim_16_beyond_512_tokens(oracle, dev, N):
     """N above the tuned kernel's 512 runs the general kernel: fp32 mask

@@ -232,3 +232,47 @@ def test_gather_bias_layout(oracle):
     assert bias.shape == (3, 343, 343)
     assert bias[2, 10, 200] == table[rpi[10, 200], 2]
     assert np.all(bias[1].diagonal() == table[1098, 1])
+
+
+def test_reference_numerics_restatement(oracle):
+    """attention_reference_numerics (the reference kernel's rounding steps):
+    with fp32 inputs nothing rounds and the online recurrence is exact, so it
+    equals the two-pass formula for any chunk size; one key gives v itself;
+    and a two-key case fixes the rounding order by hand: the numerator uses P
+    rounded to the input type, the row sum the unrounded P."""
+    import torch
+
+    g = torch.Generator().manual_seed(41)
+    B, H, N, D = 3, 2, 37, 16
+    q, k, v = (torch.randn((B, H, N, D), generator=g) for _ in range(3))
+    bias = torch.randn((H, N, N), generator=g) * 0.1
+    mask = torch.where(torch.rand((B, N, N), generator=g) > 0.8, -100.0, 0.0)
+    want = oracle.attention(q.numpy(), k.numpy(), v.numpy(), bias.numpy(), mask.numpy(), None, scale=0.3,
+                            dtype=np.float64)
+    for block in (1, 5, 32, N):
+        got = oracle.attention_reference_numerics(q, k, v, bias, mask, scale=0.3, block_n=block)
+        assert np.abs(got.numpy() - want).max() < 2e-6
+
+    for dt in (torch.float16, torch.bfloat16):
+        one = torch.randn((1, 1, 1, 8), generator=g).to(dt)
+        got = oracle.attention_reference_numerics(one, one, one, torch.zeros((1, 1, 1)), None, scale=1.0)
+        assert torch.equal(got, one)
+
+        # two keys with scores s0 = -1.1 and 0 (both queries alike): the row max
+        # is 0, P = [exp(s0), 1]; exp(s0) is not representable in the input
+        # type, and v = identity makes the output [round(exp(s0)), 1] / (exp(s0) + 1)
+        s0 = -1.1
+        qq = torch.tensor([[[[1.0, 0.0], [1.0, 0.0]]]]).to(dt)
+        kk = torch.tensor([[[[s0, 0.0], [0.0, 0.0]]]]).to(dt)
+        vv = torch.tensor([[[[1.0, 0.0], [0.0, 1.0]]]]).to(dt)
+        got = oracle.attention_reference_numerics(qq, kk, vv, torch.zeros((1, 2, 2)), None, scale=1.0)
+        s0r = float(torch.tensor(s0).to(dt))  # k is stored in dt
+        p0 = np.exp(np.float32(s0r))  # row max is the score 0 of key 1
+        num = float(torch.tensor(p0).to(dt))
+        exp0 = torch.tensor(num / (p0 + 1.0), dtype=torch.float32).to(dt)
+        exp1 = torch.tensor(1.0 / (p0 + 1.0), dtype=torch.float32).to(dt)
+        assert torch.equal(got[0, 0, 0], torch.stack([exp0, exp1]))
+        assert torch.equal(got[0, 0, 1], got[0, 0, 0])
+        # rounding P only in the row sum as well would give a different first element
+        alt = torch.tensor(num / (num + 1.0), dtype=torch.float32).to(dt)
+        assert float(torch.tensor(p0).to(dt)) != p0 and (alt != exp0 or dt == torch.bfloat16)
