@@ -873,7 +873,7 @@ struct Stage<T, NT, true, D> {
 // caller's bias tensor: lane (col, g) holds keys 16t + 4g + r of query
 // qi.  The head's [N, N] bias is read through a buffer
 // descriptor; keys past N read 0 or the next row and are replaced by -inf
-// (probability exactly 0).  Padded query rows get 0 (never stored).  In
+// (probability exactly 0).  Padded query rows repeat row N - 1.  In
 // region mode a key whose shift-region class differs from the query's on
 // an axis that the window type `code` splits gets -100.  kLog2: the tiles
 // are kept in log2 units (multiplied by log2(e)) plus the query's row offset
@@ -899,8 +899,10 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
     // instead of being hoisted out of the window loop and held in registers
     // that the attention loop needs.
     asm volatile("" : "+v"(qi), "+v"(g), "+s"(N));
-    const bool row = qi < N;
-    const int qr = row ? qi : N - 1;
+    // Padded query rows (qi >= N) build row N - 1's tiles: their Q is row
+    // N - 1's as well (the Q loads clamp the row), so they repeat that row's
+    // scores; they are never stored and never enter the row-sum check.
+    const int qr = qi < N ? qi : N - 1;
     const int rb = lead + static_cast<int>(int64_t(qr) * bsd1) * kEs;  // byte offset of the row
     const int shift = (rb & 2) * 8;                                     // 16-bit rows: 0 or 16
     const int rowb = rb & ~3;                                           // dword-aligned
@@ -909,11 +911,16 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
         cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
         cmask = uint32_t(code) * 0x01010101u;
     }
+    // a region-masked key adds -100 to its bias: in log2 units (kLog2) the
+    // mask joins the row offset, so an unmasked key's value is exactly
+    // bias * log2(e) + off
+    constexpr float kMaskAdd = kLog2 ? -100.0f * kLog2e : -100.0f;
     // words per tile: 4 fp32 keys, or the 3 dwords around 4 16-bit keys
     constexpr int kWords = kEs == 4 ? 4 : 3;
-    // Two halves of the tiles, each: all loads, then the conversions (the
-    // raw words of every tile at once would not fit next to the tiles).
-    constexpr int kHalf = (NT + 1) / 2;
+    // Three parts of the tiles, each: all loads, then the conversions (the
+    // raw words of every tile at once would not fit next to the tiles, nor
+    // those of half of them next to the first window's Q in the prologue).
+    constexpr int kHalf = (NT + 2) / 3;
 #pragma unroll
     for (int u0 = 0; u0 < NT; u0 += kHalf) {
         __builtin_amdgcn_sched_barrier(0);
@@ -941,7 +948,7 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
             // masks of all tiles would not fit the scalar registers
             __builtin_amdgcn_sched_barrier(0);
             const int k4 = 16 * t + 4 * g;  // the tile's 4 keys
-            uint32_t split = 0;  // byte r nonzero: key k4 + r is masked by the region rule
+            uint32_t split = 0;  // byte r nonzero (0..7): key k4 + r is masked by the region rule
             if constexpr (kMask == kMaskRegion)
                 split = (*reinterpret_cast<const uint32_t*>(&cls[k4]) ^ cq) & cmask;
             float v4[4];
@@ -962,17 +969,56 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float val = v4[r];
+                float add = kLog2 ? off : 0.0f;
                 if constexpr (kMask == kMaskRegion) {
-                    if ((split >> (8 * r)) & 0xffu) val += -100.0f;
+                    // 1.0 if byte r of split is nonzero, else 0.0 (byte to
+                    // float, clamped to [0, 1]: one instruction)
+                    const float masked = __builtin_amdgcn_fmed3f(
+                        static_cast<float>((split >> (8 * r)) & 0xffu), 0.0f, 1.0f);
+                    add = __builtin_fmaf(masked, kMaskAdd, add);
                 }
-                if constexpr (kLog2) val = __builtin_fmaf(val, kLog2e, off);
-                val = row ? val : 0.0f;
-                bs[t][r] = (k4 + r) < N ? val : -INFINITY;
+                bs[t][r] = kLog2 ? __builtin_fmaf(v4[r], kLog2e, add) : v4[r] + add;
+            }
+            // keys past N (only in the tile that holds key N - 1 and after
+            // it): probability exactly 0
+            if (16 * t + 16 > N) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) bs[t][r] = (k4 + r) < N ? bs[t][r] : -INFINITY;
             }
         }
     }
     __builtin_amdgcn_sched_barrier(0);
+}
+
+// Region mode, tiles in log2 units: tiles built for window type `from` made
+// those of type `to` without reading the bias again.  A key masked under one
+// type and not the other gains or loses the mask's -100 * log2(e); keys past
+// N stay -inf.  The sum is rounded once more than a fresh build's (a few
+// ulps of 144, about 1e-5 in log2 units, i.e. 1e-5 relative in the key's
+// probability) and a workgroup changes type at most 7 times.  Costs no
+// memory round trip: a fresh build waits on a scattered gather of the bias
+// rows (16 rows per load instruction), about 5 us per build at config 3.
+template <int NT>
+__device__ __forceinline__ void retype_tiles(f32x4 (&bs)[NT], int qi, int g, int N, int from, int to,
+                                             const uint8_t* cls) {
+    // opaque copies of the lane's position: the per-tile class addresses are
+    // then computed here, not hoisted out of the window loop into registers
+    asm volatile("" : "+v"(qi), "+v"(g));
+    const int qr = qi < N ? qi : N - 1;
+    const uint32_t cq = uint32_t(cls[qr]) * 0x01010101u;  // query class in every byte
+    const uint32_t mf = uint32_t(from) * 0x01010101u, mt = uint32_t(to) * 0x01010101u;
+    constexpr float kMaskAdd = -100.0f * kLog2e;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const uint32_t x = *reinterpret_cast<const uint32_t*>(&cls[16 * t + 4 * g]) ^ cq;
+        const uint32_t sf = x & mf, st = x & mt;  // byte r nonzero: key masked under from / to
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float was = __builtin_amdgcn_fmed3f(static_cast<float>((sf >> (8 * r)) & 0xffu), 0.0f, 1.0f);
+            const float now = __builtin_amdgcn_fmed3f(static_cast<float>((st >> (8 * r)) & 0xffu), 0.0f, 1.0f);
+            bs[t][r] = __builtin_fmaf(now - was, kMaskAdd, bs[t][r]);
+        }
+    }
 }
 
 template <int NT, int kMask, bool kLog2>
@@ -1279,6 +1325,9 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     X8 ones8;
 #pragma unroll
     for (int r = 0; r < 8; ++r) ones8[r] = T(1.0f);
+    // opaque: kept in registers for the window instead of rebuilt by moves
+    // before every row-sum product
+    asm volatile("" : "+v"(ones8));
 
     // P of the pair of tiles (t, t + 1), rounded to T: B operand of the
     // product below
@@ -1719,6 +1768,22 @@ swin_attention_tuned_kernel(const Params p) {
     static_assert(sizeof(q_lds) + sizeof(k_lds) + sizeof(vt_lds) + sizeof(cls_lds) <= 160 * 1024,
                   "LDS footprint exceeds the 160 KB of a gfx950 CU");
 
+    // One word of every 64-byte line of the kernel arguments, all requested
+    // before any is needed: the set-up below reads them in dependent chains
+    // (behind branches, in the walk of the type table), and every workgroup
+    // starting at once would otherwise wait for one scalar-cache miss after
+    // another (about 2 us of set-up at config 3).
+    if constexpr (kQReg) {
+        typedef const __attribute__((address_space(4))) uint32_t KWord;
+        KWord* kw = (KWord*)__builtin_amdgcn_kernarg_segment_ptr();
+        constexpr int kLines = (sizeof(Params) + 63) / 64;
+        static_assert(kLines <= 8, "kernel arguments beyond 8 lines");
+        uint32_t w[8];
+#pragma unroll
+        for (int l = 0; l < 8; ++l) w[l] = kw[16 * (l < kLines ? l : kLines - 1)];
+        asm volatile("" ::"s"(w[0]), "s"(w[1]), "s"(w[2]), "s"(w[3]), "s"(w[4]), "s"(w[5]), "s"(w[6]), "s"(w[7]));
+    }
+
     uint32_t chunk;
     if (!xcd_chunk(blockIdx.x, p.launched, p.chunks, chunk)) return;
     // chunk = (range * head blocks + head block) * groups + group: the groups
@@ -1811,6 +1876,7 @@ swin_attention_tuned_kernel(const Params p) {
         bool flag0 = window_flag(b0);
         QRaw<T> qraw;
         X8 qf = {};
+        if constexpr (kMask == kMaskRegion) __syncthreads();  // the region classes, for the first build
         {
             const WD d0 = St::template window_desc<kRecs>(p, b0, h, h0);
 #pragma unroll
@@ -1818,9 +1884,6 @@ swin_attention_tuned_kernel(const Params p) {
                 St::template dma_round<kRecs>(p, d0, k_lds[0], vt_lds[0], r, kRecs ? rec_off[r] : 0);
         }
         if (active) qraw = load_qraw<T>(p, b0, h, qi, g);
-        wait_vmem();
-        if (active) qf = q_operand<T>(qraw, qscale, g);
-        __syncthreads();  // the first window's rows and the region classes
 
         f32x4 bs[NT];
         PendingOut<T> pend;
@@ -1833,11 +1896,20 @@ swin_attention_tuned_kernel(const Params p) {
             // New bias (+ region mask) tiles are built before the next
             // window's rows are requested: the vector-memory counter retires
             // in order, so waiting for the bias loads after that request
-            // would wait for the rows as well.
+            // would wait for the rows as well.  The first window's tiles are
+            // built while its rows arrive (one wait covers both).
             if (active && (code0 != code_cur || rebuild)) {  // code is workgroup-uniform
-                build_tiles<NT, kMask, true>(bs, p, h, qi, g, code0, cls_lds, off);
+                if (kMask == kMaskRegion && !rebuild && code_cur >= 0)
+                    retype_tiles<NT>(bs, qi, g, p.N, code_cur, code0, cls_lds);
+                else
+                    build_tiles<NT, kMask, true>(bs, p, h, qi, g, code0, cls_lds, off);
                 code_cur = code0;
                 rebuild = false;
+            }
+            if (i == i0) {
+                wait_vmem();
+                if (active) qf = q_operand<T>(qraw, qscale, g);
+                __syncthreads();  // the first window's rows
             }
             if (b_out >= 0) {
                 store_out4<T>(p, pend.r, b_out, h, qi, g);
@@ -1925,7 +1997,10 @@ swin_attention_tuned_kernel(const Params p) {
         // waiting for the bias loads after that request would wait for the
         // rows as well.
         if (active && (code != code_cur || rebuild)) {  // code is workgroup-uniform
-            build_tiles<NT, kMask, sizeof(T) == 2>(bs, p, h, qi, g, code, cls_lds, off);
+            if (kMask == kMaskRegion && sizeof(T) == 2 && !rebuild && code_cur >= 0)
+                retype_tiles<NT>(bs, qi, g, p.N, code_cur, code, cls_lds);
+            else
+                build_tiles<NT, kMask, sizeof(T) == 2>(bs, p, h, qi, g, code, cls_lds, off);
             code_cur = code;
             rebuild = false;
         }
