@@ -33,7 +33,7 @@ HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
 HIP_SOURCES = [
-    "api.hip", "partition.hip", "attn_mask.hip", "attention.hip",
+    "api.hip", "partition.hip", "attn_mask.hip", "mask_tile.hip", "attention.hip",
     "attention_f16.hip", "attention_bf16.hip", "attention_f32.hip", "attention_d32.hip", "attention_wide.hip",
     "window_linear.hip",
 ]

@@ -28,6 +28,9 @@ C_ABI_SYMBOLS = (
     "crumpet_unshift_unpartition_3d_backward",
     "crumpet_compute_attn_mask_3d",
     "crumpet_fused_swin_attention",
+    "crumpet_fused_swin_attention_tiled",
+    "crumpet_attn_mask_tiles",
+    "crumpet_attn_mask_tiles_elements",
     "crumpet_fused_swin_attention_shifted",
     "crumpet_window_qkv_3d",
     "crumpet_window_proj_3d",
@@ -41,6 +44,8 @@ OP_NAMES = (
     "fused_unshift_unpartition_3d_backward",
     "fused_swin_attention",
     "fused_swin_attention_shifted",
+    "fused_swin_attention_tiled",
+    "attn_mask_tiles",
     "window_qkv_3d",
     "window_proj_3d",
 )

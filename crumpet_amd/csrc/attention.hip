@@ -47,8 +47,8 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
                   const void* v, const int64_t v_strides[4], int32_t dtype, int64_t B, int64_t Hh,
                   int64_t N, int64_t Dh, const void* bias, int32_t bias_dtype,
                   const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
-                  int64_t mask_batch, const int64_t mask_strides[3], const uint8_t* boundary,
-                  const Region* region, float scale, void* stream) {
+                  int64_t mask_batch, const int64_t mask_strides[3], const void* mask_tiles,
+                  const uint8_t* boundary, const Region* region, float scale, void* stream) {
     const int esize = dtype_size(dtype);
     if (esize == 0) return fail(CRUMPET_ERR_INVALID_ARGUMENT, "%s: unsupported dtype %d", what, dtype);
     if (B < 0 || Hh < 0 || N < 0 || Dh <= 0)
@@ -272,14 +272,29 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     p.chunks = static_cast<uint32_t>(chunks);
     p.launched = xcd_launch_count(p.chunks);
 
+    // A 16-bit mask also given in the tiled layout (crumpet_attn_mask_tiles)
+    // is read from there by the 2-byte kernels at 14 or 22 tiles with vector
+    // IO: a wave's 4 keys per lane of a key tile are then 512 contiguous
+    // bytes instead of 16 row pieces.  p.ms[0] becomes the elements of one
+    // window's block.
+    int kmask_run = kmask;
+    if (mask_tiles != nullptr && (kmask == attn::kMaskF16 || kmask == attn::kMaskBF16) &&
+        dtype != CRUMPET_DTYPE_F32 && p.vec_io && attn::multi_head_tiles(NT)) {
+        p.mask = mask_tiles;
+        p.ms[0] = int64_t(p.strips) * NT * 256;
+        p.ms[1] = 0;
+        p.ms[2] = 0;
+        kmask_run = kmask == attn::kMaskF16 ? attn::kMaskF16T : attn::kMaskBF16T;
+    }
+
     if (tuned32)
-        attn::launch_d32(p, NT, kmask, dtype, s);
+        attn::launch_d32(p, NT, kmask_run, dtype, s);
     else if (dtype == CRUMPET_DTYPE_F16)
-        attn::launch_f16(p, NT, kmask, s);
+        attn::launch_f16(p, NT, kmask_run, s);
     else if (dtype == CRUMPET_DTYPE_BF16)
-        attn::launch_bf16(p, NT, kmask, s);
+        attn::launch_bf16(p, NT, kmask_run, s);
     else
-        attn::launch_f32(p, NT, kmask, s);
+        attn::launch_f32(p, NT, kmask_run, s);
     return check_launch(what);
 }
 
@@ -296,7 +311,23 @@ extern "C" int crumpet_fused_swin_attention(
     return crumpet::run_attention("crumpet_fused_swin_attention", out, out_strides, q, q_strides,
                                   k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
                                   bias_dtype, bias_strides, mask, mask_dtype, mask_batch,
-                                  mask_strides, boundary, nullptr, scale, stream);
+                                  mask_strides, nullptr, boundary, nullptr, scale, stream);
+}
+
+extern "C" int crumpet_fused_swin_attention_tiled(
+    void* out, const int64_t out_strides[4], const void* q, const int64_t q_strides[4],
+    const void* k, const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+    int32_t dtype, int64_t B, int64_t Hh, int64_t N, int64_t Dh, const void* bias,
+    int32_t bias_dtype, const int64_t bias_strides[3], const void* mask, int32_t mask_dtype,
+    int64_t mask_batch, const int64_t mask_strides[3], const void* mask_tiles,
+    const uint8_t* boundary, float scale, void* stream) {
+    if (mask == nullptr || mask_tiles == nullptr)
+        return crumpet::fail(CRUMPET_ERR_INVALID_ARGUMENT,
+                             "crumpet_fused_swin_attention_tiled: mask and mask_tiles are required");
+    return crumpet::run_attention("crumpet_fused_swin_attention_tiled", out, out_strides, q, q_strides,
+                                  k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
+                                  bias_dtype, bias_strides, mask, mask_dtype, mask_batch,
+                                  mask_strides, mask_tiles, boundary, nullptr, scale, stream);
 }
 
 extern "C" int crumpet_fused_swin_attention_shifted(
@@ -309,6 +340,6 @@ extern "C" int crumpet_fused_swin_attention_shifted(
     const crumpet::Region rg = {D, H, W, {ws_d, ws_h, ws_w}, {ss_d, ss_h, ss_w}};
     return crumpet::run_attention("crumpet_fused_swin_attention_shifted", out, out_strides, q,
                                   q_strides, k, k_strides, v, v_strides, dtype, B, Hh, N, Dh, bias,
-                                  bias_dtype, bias_strides, nullptr, 0, 1, nullptr, nullptr, &rg,
-                                  scale, stream);
+                                  bias_dtype, bias_strides, nullptr, 0, 1, nullptr, nullptr, nullptr,
+                                  &rg, scale, stream);
 }

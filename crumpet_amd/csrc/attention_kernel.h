@@ -140,9 +140,22 @@ constexpr float kLog2e = 1.4426950408889634f;
 // stays below e^8, well inside fp16 / bf16 range.
 constexpr float kLazyMargin = 8.0f;
 
-// Mask modes (template parameter kMask).
-enum MaskKind { kNoMask = 0, kMaskF16 = 1, kMaskF32 = 2, kMaskBF16 = 3, kMaskRegion = 4 };
+// Mask modes (template parameter kMask).  kMaskF16T / kMaskBF16T: a 16-bit
+// mask tensor in the tiled layout of mask_tile.hip (one 8-byte word of 4
+// keys per lane and key tile, a wave's tile contiguous), for the 2-byte
+// tuned kernels at 14 and 22 tiles.
+enum MaskKind {
+    kNoMask = 0,
+    kMaskF16 = 1,
+    kMaskF32 = 2,
+    kMaskBF16 = 3,
+    kMaskRegion = 4,
+    kMaskF16T = 5,
+    kMaskBF16T = 6
+};
 constexpr bool mask_tensor(int kind) { return kind != kNoMask && kind != kMaskRegion; }
+constexpr bool mask_tiled(int kind) { return kind == kMaskF16T || kind == kMaskBF16T; }
+constexpr bool mask_f16(int kind) { return kind == kMaskF16 || kind == kMaskF16T; }
 
 // Window-type table of region mode: logical window index -> window.
 struct TypeTable {
@@ -1259,7 +1272,19 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     // [N, N] extent (see attend_f32 for the padding and end-of-extent rules).
     __amdgpu_buffer_rsrc_t mrsrc;
     int mvoff = 0;
-    if constexpr (kUseMask) {
+    if constexpr (kUseMask && mask_tiled(kMask)) {
+        // tiled layout (NT even): window m's block holds strips x NT/2 tile
+        // pairs x 64 lanes x 2 tiles x 4 keys; lane (col, g) of strip s reads
+        // its 4 keys of tiles 2p and 2p + 1 as 16 bytes at
+        // ((s * NT/2 + p) * 64 + 16 g + col) * 16, a wave's pair being 1 KB
+        // contiguous (p.ms[0]: elements per window block)
+        static_assert(NT % 2 == 0, "tiled masks: an even tile count");
+        const AlignedRsrc ar =
+            aligned_rsrc(static_cast<const char*>(p.mask) + int64_t(b % p.mask_batch) * p.ms[0] * 2,
+                         int64_t(p.strips) * NT * 512);
+        mrsrc = ar.rs;
+        mvoff = ar.lead + (((qi >> 4) * (NT / 2) * 64) + 16 * g + col) * 16;
+    } else if constexpr (kUseMask) {
         const int qr = qi < N ? qi : N - 1;
         const AlignedRsrc ar =
             aligned_rsrc(static_cast<const char*>(p.mask) + int64_t(b % p.mask_batch) * p.ms[0] * kMaskBytes,
@@ -1275,15 +1300,20 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
     // place when it uses them (mshift: 0 or 16 bits).  Words per tile: 2-byte
     // 3, fp32 4.
     int mshift = 0;
-    if constexpr (kUseMask && kMaskBytes == 2) {
+    if constexpr (kUseMask && kMaskBytes == 2 && !mask_tiled(kMask)) {
         mshift = (mvoff & 2) * 8;
         mvoff &= ~3;
     }
-    constexpr int kMWords = kMaskBytes == 2 ? 3 : 4;
+    constexpr int kMWords = mask_tiled(kMask) ? 2 : (kMaskBytes == 2 ? 3 : 4);
     typedef uint32_t MaskWords[kMWords];
     // the words of tile t
     auto fetch = [&](int t, MaskWords& w) {
-        if constexpr (kUseMask) {
+        if constexpr (kUseMask && mask_tiled(kMask)) {
+            // the 4 keys in place (shift 0): hw[0] = w[0], hw[1] = w[1]
+            const u32x2 v2 = __builtin_amdgcn_raw_buffer_load_b64(mrsrc, mvoff + (t >> 1) * 1024 + (t & 1) * 8, 0, 0);
+            w[0] = v2[0];
+            w[1] = v2[1];
+        } else if constexpr (kUseMask) {
             const int o = mvoff + (16 * t + 4 * g) * kMaskBytes;
             if constexpr (kMaskBytes == 2) {
                 const u32x3 v3 = __builtin_amdgcn_raw_buffer_load_b96(mrsrc, o, 0, 0);
@@ -1296,13 +1326,26 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             }
         }
     };
+    // tiled masks: the words of the tile pair (t, t + 1), t even, in one load
+    auto fetch_pair = [&](int t, MaskWords& w0, MaskWords& w1) {
+        if constexpr (kUseMask && mask_tiled(kMask)) {
+            const u32x4 v4 = __builtin_amdgcn_raw_buffer_load_b128(mrsrc, mvoff + (t >> 1) * 1024, 0, 0);
+            w0[0] = v4[0];
+            w0[1] = v4[1];
+            w1[0] = v4[2];
+            w1[1] = v4[3];
+        }
+    };
     // accumulator input of tile t: bias (+ region mask) tile with the row
     // offset, plus the mask tensor's values in log2 units (w: tile t's words)
     auto cinit = [&](int t, const MaskWords& w) -> f32x4 {
         f32x4 c = bs[t];
         if constexpr (kUseMask) {
             uint32_t hw[2] = {0u, 0u};  // 2-byte masks: the 4 keys' halves in place
-            if constexpr (kMaskBytes == 2) {
+            if constexpr (mask_tiled(kMask)) {
+                hw[0] = w[0];
+                hw[1] = w[1];
+            } else if constexpr (kMaskBytes == 2) {
                 hw[0] = __builtin_amdgcn_alignbit(w[1], w[0], mshift);
                 hw[1] = __builtin_amdgcn_alignbit(w[2], w[1], mshift);
             }
@@ -1311,7 +1354,7 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
                 float mv;
                 if constexpr (kMask == kMaskF32)
                     mv = __uint_as_float(w[r]);
-                else if constexpr (kMask == kMaskF16)
+                else if constexpr (mask_f16(kMask))
                     mv = static_cast<float>(
                         __builtin_bit_cast(_Float16, static_cast<uint16_t>(r & 1 ? hw[r >> 1] >> 16 : hw[r >> 1])));
                 else
@@ -1388,7 +1431,13 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         for (int t = 0; t < NT && t < 2 * kKAhead; ++t) kf[t] = kfrag(t);
         if constexpr (kUseMask) {
 #pragma unroll
-            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t) fetch(t, mw[t]);
+            for (int t = 0; t < NT && t < 2 * kMaskAhead; ++t) {
+                if constexpr (mask_tiled(kMask)) {
+                    if (t % 2 == 0) fetch_pair(t, mw[t], mw[t + 1]);
+                } else {
+                    fetch(t, mw[t]);
+                }
+            }
         }
 #pragma unroll
         for (int t = 0; t < NT && t < 2; ++t)
@@ -1417,7 +1466,13 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
             if constexpr (kUseMask) {
 #pragma unroll
                 for (int t = t0 + 2 * kMaskAhead; t < t0 + 2 * kMaskAhead + 2; ++t)
-                    if (t < NT) fetch(t, mw[t]);
+                    if (t < NT) {
+                        if constexpr (mask_tiled(kMask)) {
+                            if (t % 2 == 0) fetch_pair(t, mw[t], mw[t + 1]);
+                        } else {
+                            fetch(t, mw[t]);
+                        }
+                    }
             }
             X8 pb;
             if constexpr (kKAhead == 1) {
@@ -1566,6 +1621,7 @@ __device__ __forceinline__ void attend_f32(const Params& p, const f32x4 (&bs)[NT
     // then zero in-range keys sharing the load, so those lanes read that
     // tile again element by element.  Offsets are immediates.
     constexpr int kMaskBytes = (kMask == kMaskF32) ? 4 : 2;
+    static_assert(!mask_tiled(kMask), "tiled masks: 2-byte tuned kernels only");
     constexpr int kMaskWords = kMaskBytes;  // 32-bit words per lane and tile
     __amdgpu_buffer_rsrc_t mrsrc;
     int mvoff = 0;
@@ -1804,7 +1860,7 @@ swin_attention_tuned_kernel(const Params p) {
     // flag is clear, and boundary windows come in runs (the last window
     // slab of a volume is a run of nWh * nWw), so contiguous ranges would
     // leave some workgroups with mostly masked windows (17% at config 3).
-    constexpr bool kStrided = kMask == kMaskF16 || kMask == kMaskF32 || kMask == kMaskBF16;
+    constexpr bool kStrided = mask_tensor(kMask);
     const int i0 = kStrided ? 0 : range * p.win_per_wg;
     const int i1 = kStrided ? (p.B - range + p.ranges - 1) / p.ranges : min(p.B, i0 + p.win_per_wg);
 
@@ -2085,6 +2141,20 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
             hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, MK, false, 1>), grid, block, 0, s, p); \
         }                                                                                             \
     } while (0)
+// tiled 16-bit masks: 2-byte types with vector IO at 14 and 22 tiles (the
+// host selects them only there)
+#define CRUMPET_ATTN_TILED(NTV, MK)                                                                   \
+    do {                                                                                              \
+        if constexpr (v_row_major<T>() && multi_head_tiles(NTV)) {                                    \
+            if (p.vec_io) {                                                                           \
+                if (p.hpw == kHeadsPerWg)                                                             \
+                    hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, MK, true, kHeadsPerWg>), grid, \
+                                       block, 0, s, p);                                               \
+                else                                                                                  \
+                    hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NTV, MK, true, 1>), grid, block, 0, s, p); \
+            }                                                                                         \
+        }                                                                                             \
+    } while (0)
 #define CRUMPET_ATTN_NT(NTV)                                            \
     case NTV:                                                           \
         switch (kmask) {                                                \
@@ -2092,6 +2162,8 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
             case kMaskF16: CRUMPET_ATTN_MASK(NTV, kMaskF16); break;     \
             case kMaskF32: CRUMPET_ATTN_MASK(NTV, kMaskF32); break;     \
             case kMaskBF16: CRUMPET_ATTN_MASK(NTV, kMaskBF16); break;   \
+            case kMaskF16T: CRUMPET_ATTN_TILED(NTV, kMaskF16T); break;  \
+            case kMaskBF16T: CRUMPET_ATTN_TILED(NTV, kMaskBF16T); break; \
             default: CRUMPET_ATTN_MASK(NTV, kMaskRegion); break;        \
         }                                                               \
         break;
@@ -2106,6 +2178,7 @@ void launch(const Params& p, int NT, int kmask, hipStream_t s) {
         default: break;
     }
 #undef CRUMPET_ATTN_NT
+#undef CRUMPET_ATTN_TILED
 #undef CRUMPET_ATTN_MASK
 }
 
@@ -2128,6 +2201,12 @@ void launch32_slots(const Params& p, int kmask, hipStream_t s) {
             break;
         case kMaskBF16:
             hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskBF16, true, HPW, 32>), grid, block, 0, s, p);
+            break;
+        case kMaskF16T:
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskF16T, true, HPW, 32>), grid, block, 0, s, p);
+            break;
+        case kMaskBF16T:
+            hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskBF16T, true, HPW, 32>), grid, block, 0, s, p);
             break;
         default:
             hipLaunchKernelGGL((swin_attention_tuned_kernel<T, NT, kMaskRegion, true, HPW, 32>), grid, block, 0, s,

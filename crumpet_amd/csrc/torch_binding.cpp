@@ -4,8 +4,10 @@
 // (torch-ext/torch_binding.cpp:10-31), plus `fused_swin_attention`, which
 // the reference launched from Python through Triton, and
 // `fused_swin_attention_shifted` (attention with the shifted-window mask
-// derived from the volume geometry instead of a mask tensor), and the fused
-// block projections `window_qkv_3d` / `window_proj_3d`.  Every impl checks
+// derived from the volume geometry instead of a mask tensor),
+// `attn_mask_tiles` / `fused_swin_attention_tiled` (a 16-bit mask's tiled
+// copy and attention reading it), and the fused block projections
+// `window_qkv_3d` / `window_proj_3d`.  Every impl checks
 // shapes, dtypes and devices (so no launch can index outside its tensors),
 // takes the current HIP stream of the tensor's device (ROCm torch tags HIP
 // devices as "cuda", hence the masquerading guard/stream helpers) and forwards to the
@@ -124,11 +126,12 @@ void fused_unshift_unpartition_3d_backward(at::Tensor& grad_windows, const at::T
         ss_d, ss_h, ss_w, stream_of(grad_x)));
 }
 
-void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
-                          const at::Tensor& v, const at::Tensor& bias,
-                          const std::optional<at::Tensor>& mask,
-                          const std::optional<at::Tensor>& boundary, double scale) {
-    const char* what = "fused_swin_attention";
+// fused_swin_attention, and with `tiles` (the tiled copy of the mask, from
+// attn_mask_tiles) fused_swin_attention_tiled
+void run_fused_swin_attention(const char* what, at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
+                              const at::Tensor& v, const at::Tensor& bias,
+                              const std::optional<at::Tensor>& mask, const at::Tensor* tiles,
+                              const std::optional<at::Tensor>& boundary, double scale) {
     TORCH_CHECK(q.dim() == 4, what, ": q must have shape [B, H, N, D]");
     TORCH_CHECK(k.sizes() == q.sizes() && v.sizes() == q.sizes() && out.sizes() == q.sizes(), what,
                 ": q, k, v and out must have the same shape");
@@ -189,10 +192,57 @@ void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor
     // the kernels read bias rows with unit key stride, rows not overlapping
     const at::Tensor bk = (bias.stride(2) == 1 && (N < 2 || bias.stride(1) >= N)) ? bias : bias.contiguous();
     for (int i = 0; i < 3; ++i) bs[i] = bk.stride(i);
+    if (tiles != nullptr) {
+        TORCH_CHECK(mask.has_value(), what, ": mask is required");
+        TORCH_CHECK(tiles->device() == dev && tiles->scalar_type() == mask->scalar_type() &&
+                        tiles->is_contiguous() &&
+                        tiles->numel() == crumpet_attn_mask_tiles_elements(mbatch, N),
+                    what, ": mask_tiles must be attn_mask_tiles(mask)");
+        check_status(crumpet_fused_swin_attention_tiled(
+            out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
+            bk.data_ptr(), bdt, bs, mptr, mdt, mbatch, ms, tiles->data_ptr(), bptr,
+            static_cast<float>(scale), stream_of(q)));
+        return;
+    }
     check_status(crumpet_fused_swin_attention(
         out.data_ptr(), os, q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs, dt, B, Hh, N, Dh,
         bk.data_ptr(), bdt, bs, mptr, mdt, mbatch, ms, bptr, static_cast<float>(scale),
         stream_of(q)));
+}
+
+void fused_swin_attention(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
+                          const at::Tensor& v, const at::Tensor& bias,
+                          const std::optional<at::Tensor>& mask,
+                          const std::optional<at::Tensor>& boundary, double scale) {
+    run_fused_swin_attention("fused_swin_attention", out, q, k, v, bias, mask, nullptr, boundary, scale);
+}
+
+void fused_swin_attention_tiled(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
+                                const at::Tensor& v, const at::Tensor& bias, const at::Tensor& mask,
+                                const at::Tensor& mask_tiles, const std::optional<at::Tensor>& boundary,
+                                double scale) {
+    run_fused_swin_attention("fused_swin_attention_tiled", out, q, k, v, bias, mask, &mask_tiles, boundary,
+                             scale);
+}
+
+void attn_mask_tiles(at::Tensor& out, const at::Tensor& mask) {
+    const char* what = "attn_mask_tiles";
+    TORCH_CHECK(mask.dim() == 3 && mask.size(1) == mask.size(2), what, ": mask must have shape [M, N, N]");
+    const int32_t mdt = dtype_code(mask.scalar_type());
+    TORCH_CHECK(mdt == CRUMPET_DTYPE_F16 || mdt == CRUMPET_DTYPE_BF16, what,
+                ": mask dtype must be float16 or bfloat16");
+    TORCH_CHECK(out.is_cuda() && mask.is_cuda() && out.device() == mask.device(), what,
+                ": out and mask must be on the same HIP device");
+    const int64_t M = mask.size(0), N = mask.size(1);
+    const int64_t n = crumpet_attn_mask_tiles_elements(M, N);
+    TORCH_CHECK(n >= 0, what, ": N = ", N, " is outside 1 .. 512");
+    TORCH_CHECK(out.scalar_type() == mask.scalar_type() && out.is_contiguous() && out.numel() == n, what,
+                ": out must be a contiguous tensor of the mask's dtype with attn_mask_tiles_elements(M, N) elements");
+    if (n == 0) return;
+    const at::Tensor m = mask.stride(2) == 1 ? mask : mask.contiguous();
+    const int64_t ms[3] = {m.stride(0), m.stride(1), m.stride(2)};
+    const c10::hip::HIPGuardMasqueradingAsCUDA guard(mask.device());
+    check_status(crumpet_attn_mask_tiles(out.data_ptr(), m.data_ptr(), mdt, M, N, ms, stream_of(mask)));
 }
 
 void fused_swin_attention_shifted(at::Tensor& out, const at::Tensor& q, const at::Tensor& k,
@@ -353,6 +403,11 @@ TORCH_LIBRARY(crumpet_ops, ops) {
         "Tensor? mask, Tensor? boundary, float scale) -> ()",
         kCrumpetOpTags);
     ops.def(
+        "fused_swin_attention_tiled(Tensor! out, Tensor q, Tensor k, Tensor v, Tensor bias, "
+        "Tensor mask, Tensor mask_tiles, Tensor? boundary, float scale) -> ()",
+        kCrumpetOpTags);
+    ops.def("attn_mask_tiles(Tensor! out, Tensor mask) -> ()", kCrumpetOpTags);
+    ops.def(
         "fused_swin_attention_shifted(Tensor! out, Tensor q, Tensor k, Tensor v, Tensor bias, "
         "int D, int H, int W, int ws_d, int ws_h, int ws_w, int ss_d, int ss_h, int ss_w, "
         "float scale) -> ()",
@@ -376,6 +431,8 @@ TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
     ops.impl("fused_unshift_unpartition_3d_backward", &fused_unshift_unpartition_3d_backward);
     ops.impl("fused_swin_attention", &fused_swin_attention);
     ops.impl("fused_swin_attention_shifted", &fused_swin_attention_shifted);
+    ops.impl("fused_swin_attention_tiled", &fused_swin_attention_tiled);
+    ops.impl("attn_mask_tiles", &attn_mask_tiles);
     ops.impl("window_qkv_3d", &window_qkv_3d);
     ops.impl("window_proj_3d", &window_proj_3d);
 }

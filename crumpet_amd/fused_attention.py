@@ -19,9 +19,101 @@ head dims the reference's Triton kernel takes: powers of two from 16).
 
 from __future__ import annotations
 
+import ctypes
+import weakref
+from collections import OrderedDict
+
 import torch
 
 from . import _native
+
+# Tiled copies of 16-bit masks (``attn_mask_tiles``): in the tiled layout a
+# wave's mask words of one key tile are 512 contiguous bytes instead of 16
+# row pieces, which the tuned kernels read faster (config 3: about 7% of the
+# tensor-mask launch).  A copy is made the second time one mask tensor
+# object is passed and kept for the most recent masks only.  It is used
+# while that object is alive and its version counter (bumped by every
+# in-place torch op on it or on a view of it) and storage are unchanged;
+# writes that bypass torch's version counter (raw pointers, DLPack) are not
+# seen.  A new tensor, even at a recycled address, is never matched.
+_TILED_KEEP = 2
+_tiled: "OrderedDict[int, tuple]" = OrderedDict()  # id -> (weakref, stamp, tiles)
+_seen: "OrderedDict[int, tuple]" = OrderedDict()  # id -> (weakref, stamp)
+
+
+def _stamp(mask: torch.Tensor) -> tuple | None:
+    try:
+        return (mask.device, mask.data_ptr(), mask._version, tuple(mask.shape), tuple(mask.stride()), mask.dtype)
+    except (RuntimeError, NotImplementedError):  # fake / functional tensors while tracing
+        return None
+
+
+def _matches(entry, mask: torch.Tensor, stamp: tuple) -> bool:
+    return entry is not None and entry[0]() is mask and entry[1] == stamp
+
+
+def _tiles_elements(M: int, N: int) -> int:
+    f = _native.hip_library().crumpet_attn_mask_tiles_elements
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    return int(f(M, N))
+
+
+def mask_tiles(mask: torch.Tensor) -> torch.Tensor:
+    """The tiled copy of a 16-bit ``[M, N, N]`` mask that
+    ``fused_swin_attention`` reads when it can (one launch; 1 <= N <= 512)."""
+    M, N = int(mask.shape[0]), int(mask.shape[1])
+    n = _tiles_elements(M, N)
+    if n < 0:
+        raise ValueError(f"attn_mask_tiles: N = {N} is outside 1 .. 512")
+    out = torch.empty(n, dtype=mask.dtype, device=mask.device)
+    _native.ops().attn_mask_tiles(out, mask)
+    return out
+
+
+def _cached_tiles(q: torch.Tensor, mask: torch.Tensor | None) -> torch.Tensor | None:
+    """The kept tiled copy of ``mask`` for this call, or None (read the mask
+    itself): only 16-bit masks with 2-byte q at head dim 16 or 32 and
+    129 <= N <= 352 (the tuned kernels' 14- and 22-tile forms), never while
+    a graph is captured or traced."""
+    if mask is None or mask.dtype not in (torch.float16, torch.bfloat16):
+        return None
+    if q.dtype not in (torch.float16, torch.bfloat16) or q.shape[3] not in (16, 32):
+        return None
+    N = q.shape[2]
+    if not 129 <= N <= 352 or mask.dim() != 3 or mask.shape[1] != N or mask.shape[2] != N:
+        return None
+    if torch.compiler.is_compiling() or (torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()):
+        return None
+    stamp = _stamp(mask)
+    if stamp is None:
+        return None
+    key = id(mask)
+    hit = _tiled.get(key)
+    if _matches(hit, mask, stamp):
+        _tiled.move_to_end(key)
+        return hit[2]
+    if not _matches(_seen.get(key), mask, stamp):
+        _seen[key] = (weakref.ref(mask), stamp)
+        _seen.move_to_end(key)
+        while len(_seen) > 4 * _TILED_KEEP:
+            _seen.popitem(last=False)
+        return None
+    del _seen[key]
+    tiles = mask_tiles(mask)
+    _tiled[key] = (weakref.ref(mask), stamp, tiles)
+    _tiled.move_to_end(key)
+    while len(_tiled) > _TILED_KEEP:
+        _tiled.popitem(last=False)
+    return tiles
+
+
+def _attend(out, q, k, v, bias, mask, boundary, scale) -> None:
+    tiles = _cached_tiles(q, mask)
+    if tiles is not None:
+        _native.ops().fused_swin_attention_tiled(out, q, k, v, bias, mask, tiles, boundary, float(scale))
+    else:
+        _native.ops().fused_swin_attention(out, q, k, v, bias, mask, boundary, float(scale))
 
 
 def fused_swin_attention(
@@ -64,7 +156,7 @@ def fused_swin_attention(
 
     if out is None:
         out = torch.empty_like(q)
-    _native.ops().fused_swin_attention(out, q, k, v, relative_position_bias, mask, bnd, float(scale))
+    _attend(out, q, k, v, relative_position_bias, mask, bnd, scale)
     return out
 
 
@@ -82,7 +174,7 @@ def fused_swin_attention_windows(
     window position ``[nW, N, N]`` with ``nW`` dividing ``B``; window ``b``
     then reads ``mask[b % nW]`` (the layout MONAI's ``mask.repeat`` tiling
     produces, without materialising the repeat)."""
-    _native.ops().fused_swin_attention(out, q, k, v, relative_position_bias, mask, boundary, float(scale))
+    _attend(out, q, k, v, relative_position_bias, mask, boundary, scale)
     return out
 
 
@@ -124,4 +216,4 @@ def fused_swin_attention_shifted(
     return out
 
 
-__all__ = ["fused_swin_attention", "fused_swin_attention_shifted"]
+__all__ = ["fused_swin_attention", "fused_swin_attention_shifted", "mask_tiles"]

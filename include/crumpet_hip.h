@@ -202,6 +202,51 @@ CRUMPET_API int crumpet_fused_swin_attention(void* out, const int64_t out_stride
                                  void* stream);
 
 /*
+ * Tiled copy of a 16-bit mask [M, N, N] (strides in elements, unit key
+ * stride) for crumpet_fused_swin_attention_tiled:
+ *   tiles[m][s][p][16 g + c][j][r] = mask[m][min(16 s + c, N - 1)][16 (2p + j) + 4 g + r]
+ * (0 for keys past N), s < ceil(N / 16), p < NT / 2 for the attention
+ * kernel's tile count NT for N (2 where that is 1);
+ * crumpet_attn_mask_tiles_elements(M, N) elements of the mask's dtype (-1
+ * for N outside 1 .. 512), 8-byte aligned.  A lane's keys of a pair of key
+ * tiles are then 16 contiguous bytes, a wave's 1 KB.  Bits are copied.
+ *
+ * No counterpart in the reference (it reads the mask in place,
+ * torch-ext/crumpet/fused_attention.py:123-128); for callers that use one
+ * mask tensor in many calls, as the MONAI layers do with their per-layer
+ * mask (monai_patch.py:167-191).
+ */
+CRUMPET_API int64_t crumpet_attn_mask_tiles_elements(int64_t M, int64_t N);
+CRUMPET_API int crumpet_attn_mask_tiles(void* out, const void* mask, int32_t mask_dtype, int64_t M,
+                                        int64_t N, const int64_t mask_strides[3], void* stream);
+
+/*
+ * crumpet_fused_swin_attention with the mask also given as its tiled copy
+ * (crumpet_attn_mask_tiles of the same mask, same M and N).  Results are
+ * identical; the tuned kernels read the tiled copy where they run with
+ * 2-byte q/k/v, vector IO and 129 <= N <= 352 (their 14- and 22-tile
+ * forms), the mask itself otherwise.  mask and mask_tiles are required.
+ *
+ * No counterpart in the reference: a faster form of
+ * crumpet_fused_swin_attention (torch-ext/crumpet/fused_attention.py:149-226)
+ * for callers that keep the tiled copy with the mask.
+ */
+CRUMPET_API int crumpet_fused_swin_attention_tiled(void* out, const int64_t out_strides[4],
+                                 const void* q, const int64_t q_strides[4],
+                                 const void* k, const int64_t k_strides[4],
+                                 const void* v, const int64_t v_strides[4],
+                                 int32_t dtype,
+                                 int64_t B, int64_t Hh, int64_t N, int64_t Dh,
+                                 const void* bias, int32_t bias_dtype,
+                                 const int64_t bias_strides[3],
+                                 const void* mask, int32_t mask_dtype, int64_t mask_batch,
+                                 const int64_t mask_strides[3],
+                                 const void* mask_tiles,
+                                 const uint8_t* boundary,
+                                 float scale,
+                                 void* stream);
+
+/*
  * Fused window attention with the shifted-window mask of a [D, H, W] volume
  * (window ws, shift ss) instead of a mask tensor.  Bit-identical in meaning
  * to crumpet_fused_swin_attention with

@@ -86,6 +86,10 @@ def test_opcheck_attention_and_block_ops(dev):
     _opcheck(ops.fused_swin_attention.default, (out, q, k, v, bias, mask, bnd, 0.25))
     _opcheck(ops.fused_swin_attention.default, (out, q, k, v, bias, None, None, 0.25))
     _opcheck(ops.fused_swin_attention_shifted.default, (out, q, k, v, bias, 6, 6, 6, 3, 3, 3, 1, 1, 1, 0.25))
+    hmask = mask.half()
+    tiles = torch.empty(2 * 2 * 2 * 256, dtype=torch.float16, device=dev)  # M=2, N=27: 2 strips x 2 tiles
+    _opcheck(ops.attn_mask_tiles.default, (tiles, hmask))
+    _opcheck(ops.fused_swin_attention_tiled.default, (out, q, k, v, bias, hmask, tiles, bnd, 0.25))
 
     x = seeded((1, 6, 6, 6, 16), torch.float16, 8).to(dev)
     w = (seeded((48, 16), torch.float32, 9) / 4).half().to(dev)

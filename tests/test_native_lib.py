@@ -181,3 +181,19 @@ def test_dispatcher_schemas_match_reference():
         assert norm == f"crumpet_ops::{name}{sig}", schema
         assert torch.Tag.pt2_compliant_tag in getattr(ops, name).default.tags
         assert torch.Tag.needs_fixed_stride_order in getattr(ops, name).default.tags
+
+
+def test_mask_tiles_element_count():
+    """crumpet_attn_mask_tiles_elements: M x ceil(N / 16) strips x the tuned
+    kernel's tile count (made even: the layout is in tile pairs) x 256 (64
+    lanes x 4 keys), -1 outside 1 <= N <= 512 (host arithmetic only)."""
+    from crumpet_amd import _native
+
+    f = ctypes.CDLL(str(_native.HIP_LIB)).crumpet_attn_mask_tiles_elements
+    f.restype = ctypes.c_int64
+    f.argtypes = [ctypes.c_int64, ctypes.c_int64]
+    for N, strips, tiles in ((1, 1, 2), (16, 1, 2), (17, 2, 2), (129, 9, 14), (224, 14, 14), (225, 15, 22),
+                             (343, 22, 22), (352, 22, 22), (353, 23, 32), (512, 32, 32)):
+        assert f(3, N) == 3 * strips * tiles * 256, N
+    assert f(0, 343) == 0
+    assert f(1, 0) == -1 and f(1, 513) == -1 and f(-1, 343) == -1
