@@ -197,8 +197,9 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
             reinterpret_cast<uintptr_t>(ptr[i]) % (4 * esize))
             vec = false;
     }
-    // the vector staging addresses q/k/v rows of one window with 32-bit byte offsets
-    for (int i = 0; i < 3; ++i) {
+    // the vector paths address q/k/v and out rows of one (window, head) with
+    // 32-bit byte offsets
+    for (int i = 0; i < 4; ++i) {
         if (st[i][2] < 0 || ((N - 1) * st[i][2] + 16) * esize >= (int64_t(1) << 31)) vec = false;
     }
     p.vec_io = vec ? 1 : 0;

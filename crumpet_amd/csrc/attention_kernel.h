@@ -1161,10 +1161,16 @@ struct PendingOut {
 template <typename T>
 __device__ __forceinline__ void store_out4(const Params& p, const typename Frag<T>::x4& r, int b, int h, int qi,
                                            int g) {
-    if (qi < p.N) {
-        T* orow = static_cast<T*>(p.out) + b * p.os[0] + h * p.os[1] + qi * p.os[2];
-        *reinterpret_cast<typename Frag<T>::x4*>(orow + 4 * g) = r;
-    }
+    // scalar base of the (window, head) block and a 32-bit lane offset
+    char* ub = uniform_ptr(static_cast<char*>(p.out) + (int64_t(b) * p.os[0] + int64_t(h) * p.os[1]) *
+                                                           int64_t(sizeof(T)));
+    const int extent = __builtin_amdgcn_readfirstlane(
+        static_cast<int>((int64_t(p.N - 1) * p.os[2] + 16) * int64_t(sizeof(T))));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(ub, 0, extent, 0x00020000);
+    if (qi < p.N)
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, r), rs,
+                                              (qi * static_cast<int>(p.os[2]) + 4 * g) * static_cast<int>(sizeof(T)),
+                                              0, 0);
 }
 
 // Head dim 16, LDS-DMA path: a wave's Q operand never passes through LDS.
@@ -1991,7 +1997,7 @@ swin_attention_tuned_kernel(const Params p) {
                 else
                     rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, D, true>(
                         p, bs, qf, qf, kw, vw, b0, h, qi, col, g, off, issue, pend);
-                b_out = b0;
+                b_out = __builtin_amdgcn_readfirstlane(b0);
             } else {
 #pragma unroll
                 for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r) issue(r);
