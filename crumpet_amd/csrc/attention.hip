@@ -56,8 +56,8 @@ int run_attention(const char* what, void* out, const int64_t out_strides[4], con
     if (B == 0 || Hh == 0 || N == 0) return CRUMPET_OK;
     // head dim 16 with N <= 512 (every Swin UNETR stage) runs the tuned
     // kernel; other head dims and larger windows the general one
-    if (Dh != 16 && Dh != 32 && Dh != 64 && Dh != 128)
-        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: head_dim %lld is not supported (16, 32, 64 or 128)",
+    if (Dh != 16 && Dh != 32 && Dh != 64 && Dh != 128 && Dh != 256)
+        return fail(CRUMPET_ERR_UNSUPPORTED, "%s: head_dim %lld is not supported (16, 32, 64, 128 or 256)",
                     what, (long long)Dh);
     // The tuned kernel feeds q * scale * log2(e) to the score product (its
     // scores come out in log2 units).  An fp16 q is at most 65504, so that

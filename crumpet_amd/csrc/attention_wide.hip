@@ -1,6 +1,7 @@
 // General fused window attention for the shapes the head-dim-16 kernel does
-// not cover: head dims 32, 64 and 128, and windows of more than 512 tokens
-// (any head dim of 16..128 that is a power of two, any N).  Same contract
+// not cover: head dims 32, 64, 128 and 256, and windows of more than 512
+// tokens (any head dim of 16..256 that is a power of two, any N).  At head
+// dim 256 a wave holds about 330 registers (one wave per SIMD).  Same contract
 // and the same three mask modes as swin_attention_tuned_kernel
 // (attention_kernel.h); the numerics are the reference's:
 //
@@ -426,7 +427,8 @@ void launch_t(const Params& p, int Dh, int mode, int32_t mask_dtype, uint32_t qb
         case 16: launch_d<T, 16>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
         case 32: launch_d<T, 32>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
         case 64: launch_d<T, 64>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
-        default: launch_d<T, 128>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
+        case 128: launch_d<T, 128>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
+        default: launch_d<T, 256>(p, mode, mask_dtype, qblocks, chunks, launched, s); break;
     }
 }
 

@@ -13,8 +13,8 @@ copies are needed) and writes ``out`` through its strides.  ``block_m`` and
 ``block_n`` are accepted for API compatibility; the HIP kernels' tiling is
 fixed by the MFMA shape (16-query strips, 16-key tiles).  Head dim 16 with
 up to 512 tokens per window (every Swin UNETR stage) runs the tuned kernel;
-head dims 32, 64 and 128, and larger windows, run the general kernel (the
-head dims the reference's Triton kernel takes: powers of two from 16).
+head dims 32, 64, 128 and 256, and larger windows, run the general kernel
+(the head dims the reference's Triton kernel takes: powers of two from 16).
 """
 
 from __future__ import annotations

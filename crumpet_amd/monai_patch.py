@@ -18,8 +18,8 @@ the originals; True / False likewise) replace
   -> @ v`` chain becomes one gfx950 kernel call (reference :117-198).  It
   falls back to the original in training mode, with attention dropout,
   when ``CRUMPET_DISABLE_FUSED_ATTN=1``, or for a head dimension other
-  than 16, 32, 64 or 128 (the kernels' head dimensions; every stage of the
-  feature-size-48 Swin UNETR has 16, feature size 96 gives 32).  The
+  than 16, 32, 64, 128 or 256 (the kernels' head dimensions; every stage of
+  the feature-size-48 Swin UNETR has 16, feature size 96 gives 32).  The
   reference takes the fused path for any head dimension from 16 up
   (reference :144-149), which its Triton kernel compiles for powers of two.
 
@@ -106,7 +106,7 @@ def _compute_dtype(x: torch.Tensor) -> torch.dtype:
 
 _ESIZE = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
 # head dimensions of the fused attention kernels
-_HEAD_DIMS = (16, 32, 64, 128)
+_HEAD_DIMS = (16, 32, 64, 128, 256)
 
 
 def _fits_staging_tile(c: int, esize: int) -> bool:

@@ -177,7 +177,7 @@ CRUMPET_API int crumpet_compute_attn_mask_3d(void* out, int32_t dtype,
  *
  * Needs no workspace: every buffer is an input or the output.
  *
- * Supported: Dh = 16, 32, 64 or 128 and any N >= 1.  Dh = 16 with N <= 512
+ * Supported: Dh = 16, 32, 64, 128 or 256 and any N >= 1.  Dh = 16 with N <= 512
  * (every Swin UNETR stage at feature size 48) runs the tuned kernel; other
  * shapes run the general kernel, whose shifted-window mode below takes
  * windows of up to 2048 tokens.

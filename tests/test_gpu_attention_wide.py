@@ -60,7 +60,7 @@ def test_head_dims_shifted_mask_with_boundary(oracle, dev, Dh, dtype):
     _compare(out, ref, dtype, f"Dh={Dh} {dtype} tensor mask")
 
 
-@pytest.mark.parametrize("Dh", [32, 64, 128])
+@pytest.mark.parametrize("Dh", [32, 64, 128, 256])
 @pytest.mark.parametrize("N", [1, 27, 64, 65, 216])
 def test_head_dims_no_mask_default_scale(oracle, dev, Dh, N):
     """No mask, the default scale Dh^-0.5, key counts around the 64-key
@@ -216,6 +216,31 @@ def test_head_dim_16_beyond_512_tokens(oracle, dev, N):
     out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), bnd.to(dev),
                                scale=0.25)
     _compare(out, ref, dtype, f"N={N}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_head_dim_256_masks(oracle, dev, dtype):
+    """Head dim 256 (the largest power of two the general kernel takes; the
+    reference's Triton kernel compiles for any) at the model's scale
+    Dh^-0.5: the tensor mask with boundary flags and the shifted-window
+    regions of a 14^3 volume, N = 343."""
+    D, ws, ss, Dh = 14, (7, 7, 7), (3, 3, 3), 256
+    B, H, N = 16, 1, 343
+    print(f"head dim 256 {dtype}", flush=True)
+    q, k, v = _inputs(B, H, N, Dh, dtype, 3700)
+    bias = bias_from_table(trunc_normal_table(2197, H, 3701), ws)
+    m = oracle.attn_mask(D, D, D, ws, ss, "float32")
+    mask = torch.from_numpy(m).to(dtype).repeat(2, 1, 1)
+    bnd = boundary_flags(D, D, D, ws, ss, outer=2)
+    scale = Dh ** -0.5
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), _f32(mask), bnd.numpy(), scale=scale)
+    out = fused_swin_attention(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), mask.to(dev), bnd.to(dev),
+                               scale=scale)
+    _compare(out, ref, dtype, f"Dh=256 {dtype} tensor mask")
+    ref = oracle.attention(_f32(q), _f32(k), _f32(v), _f32(bias), m, None, scale=scale)
+    out = fused_swin_attention_shifted(q.to(dev), k.to(dev), v.to(dev), bias.to(dev), (D, D, D), ws, ss,
+                                       scale=scale)
+    _compare(out, ref, dtype, f"Dh=256 {dtype} regions")
 
 
 def test_unsupported_head_dim_raises(dev):
