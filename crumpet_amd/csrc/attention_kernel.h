@@ -930,10 +930,9 @@ __device__ __forceinline__ void build_tiles_es(f32x4 (&bs)[NT], __amdgpu_buffer_
     constexpr float kMaskAdd = kLog2 ? -100.0f * kLog2e : -100.0f;
     // words per tile: 4 fp32 keys, or the 3 dwords around 4 16-bit keys
     constexpr int kWords = kEs == 4 ? 4 : 3;
-    // Three parts of the tiles, each: all loads, then the conversions (the
-    // raw words of every tile at once would not fit next to the tiles, nor
-    // those of half of them next to the first window's Q in the prologue).
-    constexpr int kHalf = (NT + 2) / 3;
+    // Two halves of the tiles, each: all loads, then the conversions (the
+    // raw words of every tile at once would not fit next to the tiles).
+    constexpr int kHalf = (NT + 1) / 2;
 #pragma unroll
     for (int u0 = 0; u0 < NT; u0 += kHalf) {
         __builtin_amdgcn_sched_barrier(0);
