@@ -1948,9 +1948,23 @@ swin_attention_tuned_kernel(const Params p) {
 
         f32x4 bs[NT];
         PendingOut<T> pend;
-        int b_out = -1;  // the window whose output pend holds, or -1 (wave-uniform)
         int code_cur = -1;
         bool rebuild = false;  // this wave's offsets moved: rebuild its tiles (wave-uniform)
+        // The window after b0 (b1, ...) with its DMA descriptor, and its Q
+        // rows requested, are prepared before the barrier that ends the
+        // window before it: waves that finish their pair loop early do that
+        // scalar work while the others compute, and the window top after the
+        // barrier goes straight into the next pair loop.
+        int b1 = b0, code1 = code0;
+        bool flag1 = flag0;
+        WD d1 = {};
+        auto prepare_next = [&]() {
+            it.next(p);
+            b1 = it.window(p, code1);
+            flag1 = window_flag(b1);
+            d1 = St::template window_desc<kRecs>(p, b1, h, h0);
+            if (active) qraw = load_qraw<T>(p, b1, h, qi, g);
+        };
         for (int i = i0; i < i1; ++i) {
             const int buf = (i - i0) & 1;
             const bool more = i + 1 < i1;
@@ -1970,21 +1984,8 @@ swin_attention_tuned_kernel(const Params p) {
             if (i == i0) {
                 wait_vmem();
                 if (active) qf = q_operand<T>(qraw, qscale, g);
+                if (more) prepare_next();
                 __syncthreads();  // the first window's rows
-            }
-            if (b_out >= 0) {
-                store_out4<T>(p, pend.r, b_out, h, qi, g);
-                b_out = -1;
-            }
-            int b1 = b0, code1 = code0;
-            bool flag1 = flag0;
-            WD d1 = {};
-            if (more) {
-                it.next(p);
-                b1 = it.window(p, code1);
-                flag1 = window_flag(b1);
-                d1 = St::template window_desc<kRecs>(p, b1, h, h0);
-                if (active) qraw = load_qraw<T>(p, b1, h, qi, g);
             }
             const DmaIssuer<T, St, kRecs, kStageWaves> issue{&p, d1, k_lds[buf ^ 1], vt_lds[buf ^ 1], rec_off, more};
             T* const kw = k_lds[buf] + (kRecs ? 16 * slot : 0);  // this head's rows of each record
@@ -1996,19 +1997,22 @@ swin_attention_tuned_kernel(const Params p) {
                 else
                     rebuild = attend_offset<T, NT, kMask, false, kVec, kRecs, D, true>(
                         p, bs, qf, qf, kw, vw, b0, h, qi, col, g, off, issue, pend);
-                b_out = __builtin_amdgcn_readfirstlane(b0);
             } else {
 #pragma unroll
                 for (int r = 0; r < St::template dma_rounds<kRecs>(); ++r) issue(r);
             }
             wait_vmem();  // this wave's DMA rows (and its Q) have landed
-            if (active && more) qf = q_operand<T>(qraw, qscale, g);
-            __syncthreads();
+            if (active) {
+                if (more) qf = q_operand<T>(qraw, qscale, g);
+                // after the wait: the store then retires during the next window
+                store_out4<T>(p, pend.r, b0, h, qi, g);
+            }
             b0 = b1;
             code0 = code1;
             flag0 = flag1;
+            if (i + 2 < i1) prepare_next();
+            __syncthreads();
         }
-        if (b_out >= 0) store_out4<T>(p, pend.r, b_out, h, qi, g);
         return;
     }
 
