@@ -71,17 +71,29 @@ def parse():
 
 
 def _events_time(fn, iters):
-    """Average ms per call of fn over iters back-to-back calls, HIP events on the current stream."""
+    """Average ms per call of fn over iters back-to-back calls, HIP events on
+    the current stream.  Python's cyclic garbage collector is paused over the
+    timed calls (as timeit does): a full collection in a process holding a
+    model takes tens of milliseconds and would land in whichever call
+    happened to trigger it."""
+    import gc
+
     import torch
 
     s = torch.cuda.Event(enable_timing=True)
     e = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    s.record()
-    for i in range(iters):
-        fn(i)
-    e.record()
-    torch.cuda.synchronize()
+    enabled = gc.isenabled()
+    gc.disable()
+    try:
+        s.record()
+        for i in range(iters):
+            fn(i)
+        e.record()
+        torch.cuda.synchronize()
+    finally:
+        if enabled:
+            gc.enable()
     return s.elapsed_time(e) / iters
 
 

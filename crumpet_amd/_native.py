@@ -48,6 +48,7 @@ OP_NAMES = (
     "attn_mask_tiles",
     "window_qkv_3d",
     "window_proj_3d",
+    "window_msa_3d",
 )
 
 _hip = None
@@ -78,17 +79,27 @@ def _load() -> None:
 
 
 def _mutating_op_fake(*args, **kwargs) -> None:
-    """Every crumpet_ops op writes into a caller-allocated output and returns
-    nothing, so its fake (meta) kernel has nothing to do."""
+    """The crumpet_ops ops other than window_msa_3d write into a
+    caller-allocated output and return nothing, so their fake (meta) kernel
+    has nothing to do."""
     return None
+
+
+def _window_msa_fake(x, norm_weight, norm_bias, eps, w_qkv, b_qkv, w_proj, b_proj, bias, heads, scale,
+                     ws_d, ws_h, ws_w, ss_d, ss_h, ss_w):
+    """window_msa_3d returns the block half's output, [B, D, H, W, C_out] in
+    the weights' dtype."""
+    B, D, H, W, _ = x.shape
+    return x.new_empty((B, D, H, W, w_proj.shape[0]), dtype=w_qkv.dtype)
 
 
 def _declare_fake_kernels() -> None:
     """Fake kernels for FakeTensor / torch.compile tracing of the ops (the
     reference registers the same no-op fakes: torch-ext/crumpet/__init__.py:50-73)."""
     for name in OP_NAMES:
+        fake = _window_msa_fake if name == "window_msa_3d" else _mutating_op_fake
         try:
-            torch.library.register_fake(f"crumpet_ops::{name}")(_mutating_op_fake)
+            torch.library.register_fake(f"crumpet_ops::{name}")(fake)
         except (RuntimeError, ValueError):
             pass  # already registered in this process
 

@@ -6,8 +6,9 @@
 // `fused_swin_attention_shifted` (attention with the shifted-window mask
 // derived from the volume geometry instead of a mask tensor),
 // `attn_mask_tiles` / `fused_swin_attention_tiled` (a 16-bit mask's tiled
-// copy and attention reading it), and the fused block projections
-// `window_qkv_3d` / `window_proj_3d`.  Every impl checks
+// copy and attention reading it), the fused block projections
+// `window_qkv_3d` / `window_proj_3d`, and `window_msa_3d`, which runs those
+// three kernels for a whole block half in one dispatcher call.  Every impl checks
 // shapes, dtypes and devices (so no launch can index outside its tensors),
 // takes the current HIP stream of the tensor's device (ROCm torch tags HIP
 // devices as "cuda", hence the masquerading guard/stream helpers) and forwards to the
@@ -375,6 +376,52 @@ void window_proj_3d(at::Tensor& out, const at::Tensor& windows, const at::Tensor
                                         stream_of(out)));
 }
 
+// The attention half of a Swin block (norm1, pad to the window grid, roll,
+// partition, qkv -> window attention -> proj, reverse, roll back, crop) as
+// one call: window_qkv_3d, the fused attention and window_proj_3d launched
+// back to back, with the qkv and attention intermediates allocated here.
+// A call from Python then costs one dispatch instead of three plus the
+// allocations and views between them, which is most of a block's time at
+// the deep stages.  A nonzero shift takes the shifted-window mask from the
+// padded volume's geometry (fused_swin_attention_shifted); without a shift
+// there is no mask.  Weights are in the compute dtype, which the outputs
+// take.
+at::Tensor window_msa_3d(const at::Tensor& x, const std::optional<at::Tensor>& norm_weight,
+                         const std::optional<at::Tensor>& norm_bias, double eps, const at::Tensor& w_qkv,
+                         const std::optional<at::Tensor>& b_qkv, const at::Tensor& w_proj,
+                         const std::optional<at::Tensor>& b_proj, const at::Tensor& bias, int64_t heads,
+                         double scale, int64_t ws_d, int64_t ws_h, int64_t ws_w, int64_t ss_d, int64_t ss_h,
+                         int64_t ss_w) {
+    const char* what = "window_msa_3d";
+    TORCH_CHECK(x.dim() == 5, what, ": x must have shape [B, D, H, W, C]");
+    TORCH_CHECK(w_qkv.dim() == 2 && w_qkv.size(0) % 3 == 0, what, ": w_qkv must have shape [3 C, C_in]");
+    const int64_t Ca = w_qkv.size(0) / 3;  // attention width
+    TORCH_CHECK(heads > 0 && Ca % heads == 0, what, ": heads must divide the attention width");
+    TORCH_CHECK(w_proj.dim() == 2, what, ": w_proj must have shape [C_out, C]");
+    TORCH_CHECK(ws_d > 0 && ws_h > 0 && ws_w > 0, what, ": window_size values must be positive");
+    const int64_t B = x.size(0), D = x.size(1), H = x.size(2), W = x.size(3);
+    const int64_t Dp = (D + ws_d - 1) / ws_d * ws_d, Hp = (H + ws_h - 1) / ws_h * ws_h,
+                  Wp = (W + ws_w - 1) / ws_w * ws_w;
+    const int64_t nwin = B * (Dp / ws_d) * (Hp / ws_h) * (Wp / ws_w), n = ws_d * ws_h * ws_w;
+    const auto opts = x.options().dtype(w_qkv.scalar_type());
+    at::Tensor qkv = at::empty({nwin, n, 3 * Ca}, opts);
+    window_qkv_3d(qkv, x.contiguous(), norm_weight, norm_bias, eps, true, w_qkv, b_qkv, ws_d, ws_h, ws_w, ss_d,
+                  ss_h, ss_w);
+    // q, k, v: [nwin, heads, n, hd] views of the [token][3][heads][hd] rows
+    const at::Tensor t = qkv.view({nwin, n, 3, heads, Ca / heads}).permute({2, 0, 3, 1, 4});
+    at::Tensor attn = at::empty({nwin, n, heads, Ca / heads}, opts);
+    at::Tensor ov = attn.permute({0, 2, 1, 3});
+    if (ss_d > 0 || ss_h > 0 || ss_w > 0)
+        fused_swin_attention_shifted(ov, t.select(0, 0), t.select(0, 1), t.select(0, 2), bias, Dp, Hp, Wp, ws_d,
+                                     ws_h, ws_w, ss_d, ss_h, ss_w, scale);
+    else
+        fused_swin_attention(ov, t.select(0, 0), t.select(0, 1), t.select(0, 2), bias, std::nullopt,
+                             std::nullopt, scale);
+    at::Tensor y = at::empty({B, D, H, W, w_proj.size(0)}, opts);
+    window_proj_3d(y, attn.view({nwin, n, Ca}), w_proj, b_proj, ws_d, ws_h, ws_w, ss_d, ss_h, ss_w);
+    return y;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(crumpet_ops, ops) {
@@ -421,6 +468,11 @@ TORCH_LIBRARY(crumpet_ops, ops) {
         "window_proj_3d(Tensor! out, Tensor windows, Tensor weight, Tensor? bias, int ws_d, int ws_h, "
         "int ws_w, int ss_d, int ss_h, int ss_w) -> ()",
         kCrumpetOpTags);
+    ops.def(
+        "window_msa_3d(Tensor x, Tensor? norm_weight, Tensor? norm_bias, float eps, Tensor w_qkv, "
+        "Tensor? b_qkv, Tensor w_proj, Tensor? b_proj, Tensor bias, int heads, float scale, int ws_d, "
+        "int ws_h, int ws_w, int ss_d, int ss_h, int ss_w) -> Tensor",
+        kCrumpetOpTags);
 }
 
 TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
@@ -435,4 +487,5 @@ TORCH_LIBRARY_IMPL(crumpet_ops, CUDA, ops) {
     ops.impl("attn_mask_tiles", &attn_mask_tiles);
     ops.impl("window_qkv_3d", &window_qkv_3d);
     ops.impl("window_proj_3d", &window_proj_3d);
+    ops.impl("window_msa_3d", &window_msa_3d);
 }

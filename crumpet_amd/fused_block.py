@@ -30,7 +30,7 @@ import torch
 
 from . import _native
 from ._geometry import as_triple, padded_dims, require_float_dtype
-from .fused_attention import fused_swin_attention_shifted, fused_swin_attention_windows
+from .fused_attention import fused_swin_attention_windows
 
 def _check(x: torch.Tensor, what: str) -> None:
     if x.device.type != "cuda":
@@ -131,24 +131,33 @@ def fused_window_msa_3d(
     ``mask`` (``[nW, N, N]``, window b reads ``mask[b mod nW]``).  ``qkv`` and
     ``proj`` are Linear modules or ``(weight, bias)`` pairs; weights already
     in ``dtype`` and contiguous are used as they are (no cast kernel).
+    Without a mask tensor the three kernels run from one dispatcher call
+    (``window_msa_3d``); with one, the boundary flags are computed and the
+    kernels are called one by one.
     """
     ws = as_triple("window_size", window_size, signed=True)
     ss = as_triple("shift_size", shift_size, signed=True)
     B, D, H, W, C = x.shape
     dtype = x.dtype if dtype is None else dtype
-    hd = C // num_heads
-    padded = padded_dims((D, H, W), ws)
-    n = ws[0] * ws[1] * ws[2]
     wq, bq = _linear(qkv)
     wp, bp = _linear(proj)
+    shifted = any(s > 0 for s in ss)
+    if region or not shifted:
+        # the three kernels in one dispatcher call (window_msa_3d), which
+        # allocates the qkv and attention intermediates itself
+        _check(x, "fused_window_msa_3d")
+        require_float_dtype(dtype)
+        wq, bq, wp, bp = (None if t is None else t.to(dtype).contiguous() for t in (wq, bq, wp, bp))
+        return _native.ops().window_msa_3d(x, norm.weight, norm.bias, float(norm.eps), wq, bq, wp, bp,
+                                           relative_position_bias, int(num_heads), float(scale), *ws, *ss)
+    hd = C // num_heads
+    n = ws[0] * ws[1] * ws[2]
     qkv_out = window_qkv_3d(x, wq, bq, ws, ss, norm.weight, norm.bias, norm.eps, True, dtype)
     nwin = qkv_out.shape[0]
     t = qkv_out.view(nwin, n, 3, num_heads, hd).permute(2, 0, 3, 1, 4)
     attn = torch.empty((nwin, n, num_heads, hd), dtype=dtype, device=x.device)
     ov = attn.permute(0, 2, 1, 3)
-    if any(s > 0 for s in ss) and region:
-        fused_swin_attention_shifted(t[0], t[1], t[2], relative_position_bias, padded, ws, ss, scale, ov)
-    elif any(s > 0 for s in ss) and mask is not None:
+    if mask is not None:
         nw = mask.shape[0]
         flags = (mask.reshape(nw, -1).abs().amax(dim=1) > 0).to(torch.uint8)
         fused_swin_attention_windows(t[0], t[1], t[2], relative_position_bias, mask,

@@ -171,22 +171,29 @@ def _window_bias(attn, n):
     return _cached(attn, ("bias", n), (attn.relative_position_bias_table, attn.relative_position_index), make)
 
 
-def _cast_linear(lin, dtype):
-    """``(weight, bias)`` of a Linear in ``dtype``, contiguous, as autocast
-    casts them for the forward; cached on the module (``_cached``)."""
+def _block_params(attn, n, dtype):
+    """``(bias, (w_qkv, b_qkv), (w_proj, b_proj))`` of a window-attention
+    module for the fused block: the gathered ``[heads, n, n]`` bias and both
+    projections cast to ``dtype``, kept as one entry on the module
+    (``_cached``), so a call checks the sources' versions once."""
     def make():
-        return (lin.weight.to(dtype).contiguous(),
-                lin.bias.to(dtype).contiguous() if lin.bias is not None else None)
+        idx = attn.relative_position_index[:n, :n].reshape(-1)
+        bias = attn.relative_position_bias_table.t()[:, idx].view(attn.num_heads, n, n)
+        cast = lambda t: None if t is None else t.to(dtype).contiguous()  # noqa: E731
+        return bias, (cast(attn.qkv.weight), cast(attn.qkv.bias)), (cast(attn.proj.weight), cast(attn.proj.bias))
 
-    sources = (lin.weight,) if lin.bias is None else (lin.weight, lin.bias)
-    return _cached(lin, ("cast", dtype), sources, make)
+    sources = tuple(t for t in (attn.relative_position_bias_table, attn.relative_position_index,
+                                attn.qkv.weight, attn.qkv.bias, attn.proj.weight, attn.proj.bias)
+                    if t is not None)
+    return _cached(attn, ("block", n, dtype), sources, make)
 
 
 def _fused_block_forward(block, x, mask_matrix, swin):
     """forward_part1 as three kernels: window_qkv_3d (norm1, pad, shift,
     partition, qkv), the fused attention, window_proj_3d (proj, reverse,
-    unshift, crop).  The gathered bias and the cast projection weights are
-    cached per module, so a call launches just the three kernels."""
+    unshift, crop), launched by one dispatcher call unless a mask tensor
+    without the geometry tag is passed.  The gathered bias and the cast
+    projection weights are cached per module."""
     b, d, h, w, c = x.shape
     window_size, shift_size = swin.get_window_size((d, h, w), block.window_size, block.shift_size)
     ws = _as_triple(window_size)
@@ -195,11 +202,10 @@ def _fused_block_forward(block, x, mask_matrix, swin):
     attn = block.attn
     n = ws[0] * ws[1] * ws[2]
     dtype = _compute_dtype(x)
-    bias = _window_bias(attn, n)
+    bias, qkv, proj = _block_params(attn, n, dtype)
     shifted = any(s > 0 for s in ss)
     region = shifted and getattr(mask_matrix, _GEOMETRY_ATTR, None) == (*padded, ws, ss)
-    return fused_window_msa_3d(x, block.norm1, _cast_linear(attn.qkv, dtype), _cast_linear(attn.proj, dtype),
-                               bias, attn.num_heads, attn.scale, ws, ss,
+    return fused_window_msa_3d(x, block.norm1, qkv, proj, bias, attn.num_heads, attn.scale, ws, ss,
                                mask=mask_matrix if shifted else None, region=region, dtype=dtype)
 
 

@@ -101,3 +101,5 @@ def test_opcheck_attention_and_block_ops(dev):
     wp = (seeded((16, 16), torch.float32, 11) / 4).half().to(dev)
     y = torch.empty((1, 6, 6, 6, 16), dtype=torch.float16, device=dev)
     _opcheck(ops.window_proj_3d.default, (y, qo[:, :, :16].contiguous(), wp, None, 3, 3, 3, 1, 1, 1))
+    rb = (seeded((1, 27, 27), torch.float32, 12) * 0.1).to(dev)
+    _opcheck(ops.window_msa_3d.default, (x, nw, nb, 1e-5, w, b, wp, None, rb, 1, 0.25, 3, 3, 3, 1, 1, 1))

@@ -344,3 +344,43 @@ def test_fused_forward_part1_matches_eager(dev, dims, dim, heads, shift, autocas
     scale = want.abs().max().item()
     print(f"forward_part1 {dims} C={dim} autocast={autocast}: max-abs {err:.2e} (max {scale:.2f})", flush=True)
     assert err < (1e-2 * scale if autocast else 1e-4 * max(1.0, scale))
+
+
+@pytest.mark.parametrize("cdt", [torch.float16, torch.bfloat16, torch.float32], ids=["f16", "bf16", "f32"])
+@pytest.mark.parametrize("dims,C,heads,ws,ss", [((9, 10, 11), 48, 3, (7, 7, 7), (3, 3, 3)),
+                                                 ((14, 14, 14), 96, 6, (7, 7, 7), (3, 3, 3)),
+                                                 ((6, 6, 6), 192, 12, (6, 6, 6), (0, 0, 0))],
+                         ids=["padded-shifted", "s1-shifted", "6cubed-noshift"])
+def test_window_msa_op_equals_the_three_calls(dev, dims, C, heads, ws, ss, cdt):
+    """window_msa_3d (one dispatcher call) runs the same three kernels as
+    window_qkv_3d -> fused_swin_attention[_shifted] -> window_proj_3d called
+    one by one: bit-identical output."""
+    _skip_unsupported(C, cdt)
+    print(f"window_msa_3d {dims} C={C} {cdt}", flush=True)
+    B = 2
+    x = seeded((B,) + dims + (C,), torch.float32, 70 + C).to(dev)
+    wq = (seeded((3 * C, C), torch.float32, 71) / C ** 0.5).to(cdt).to(dev)
+    bq = (seeded((3 * C,), torch.float32, 72) * 0.1).to(cdt).to(dev)
+    wp = (seeded((C, C), torch.float32, 73) / C ** 0.5).to(cdt).to(dev)
+    bp = (seeded((C,), torch.float32, 74) * 0.1).to(cdt).to(dev)
+    nw = (1.0 + 0.1 * seeded((C,), torch.float32, 75)).to(dev)
+    nb = (0.1 * seeded((C,), torch.float32, 76)).to(dev)
+    n = ws[0] * ws[1] * ws[2]
+    bias = (seeded((heads, n, n), torch.float32, 77) * 0.1).to(dev)
+    scale = (C // heads) ** -0.5
+    got = torch.ops.crumpet_ops.window_msa_3d(x, nw, nb, 1e-5, wq, bq, wp, bp, bias, heads, scale, *ws, *ss)
+
+    qkv = fused_block.window_qkv_3d(x, wq, bq, ws, ss, nw, nb, 1e-5, True, cdt)
+    nwin = qkv.shape[0]
+    t = qkv.view(nwin, n, 3, heads, C // heads).permute(2, 0, 3, 1, 4)
+    attn = torch.empty((nwin, n, heads, C // heads), dtype=cdt, device=dev)
+    ov = attn.permute(0, 2, 1, 3)
+    ops = torch.ops.crumpet_ops
+    if any(ss):
+        padded = tuple(-(-d // w) * w for d, w in zip(dims, ws))
+        ops.fused_swin_attention_shifted(ov, t[0], t[1], t[2], bias, *padded, *ws, *ss, scale)
+    else:
+        ops.fused_swin_attention(ov, t[0], t[1], t[2], bias, None, None, scale)
+    want = fused_block.window_proj_3d(attn.view(nwin, n, C), wp, bp, B, *dims, ws, ss)
+    assert got.dtype == cdt and got.shape == (B,) + dims + (C,)
+    assert torch.equal(got, want)

@@ -102,3 +102,39 @@ def test_graph_replays_fused_block_projections(dev):
         torch.cuda.synchronize()
         assert torch.equal(qkv, e_qkv), seed
         assert torch.equal(y, e_y), seed
+
+
+def test_graph_replays_window_msa_op(dev):
+    """window_msa_3d allocates its intermediates and output inside the call:
+    captured, they come from the graph's pool, and every replay matches an
+    eager call on the same input."""
+    C, H = 48, 3
+    x = seeded((2, 12, 12, 12, C), torch.float32, 40).to(dev)
+    w = (seeded((3 * C, C), torch.float32, 41) / C ** 0.5).half().to(dev)
+    b = (seeded((3 * C,), torch.float32, 42) * 0.1).half().to(dev)
+    wp = (seeded((C, C), torch.float32, 43) / C ** 0.5).half().to(dev)
+    gw = torch.ones(C, device=dev)
+    gb = torch.zeros(C, device=dev)
+    bias = (seeded((H, 343, 343), torch.float32, 44) * 0.1).to(dev)
+    ops = torch.ops.crumpet_ops
+
+    def run():
+        return ops.window_msa_3d(x, gw, gb, 1e-5, w, b, wp, None, bias, H, 0.25, 7, 7, 7, 3, 3, 3)
+
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        y = run()
+    torch.cuda.synchronize()
+    for seed in (50, 51, 52):
+        x.copy_(seeded(tuple(x.shape), torch.float32, seed).to(dev))
+        g.replay()
+        torch.cuda.synchronize()
+        want = run()  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), seed

@@ -107,29 +107,42 @@ def test_patched_basic_layer_bf16_autocast(patched, dev, dims, dim, heads, block
 @pytest.mark.parametrize("fused_block_on", [True, False], ids=["fused-block", "unfused-block"])
 def test_region_mode_reads_no_mask(patched, dev, monkeypatch, fused_block_on):
     """A shifted block under the patched BasicLayer takes the geometry path,
-    with and without the fused block projections."""
-    from crumpet_amd import fused_block
+    with and without the fused block projections (the fused block runs its
+    kernels through the one-call window_msa_3d op, whose shift selects the
+    geometry mask)."""
+    from crumpet_amd import _native, fused_block
 
     monkeypatch.setenv("CRUMPET_DISABLE_FUSED_BLOCK", "0" if fused_block_on else "1")
     calls = []
-    for mod in (monai_patch, fused_block):
-        real_w, real_s = mod.fused_swin_attention_windows, mod.fused_swin_attention_shifted
+    real_ops = _native.ops
 
-        def spy_w(q, k, v, bias, mask, boundary, scale, out, _real=real_w):
-            calls.append("tensor" if mask is not None else "none")
-            return _real(q, k, v, bias, mask, boundary, scale, out)
+    class OpsSpy:
+        def window_msa_3d(self, *args):
+            calls.append("msa-region" if any(args[-3:]) else "msa-none")
+            return real_ops().window_msa_3d(*args)
 
-        def spy_s(*args, _real=real_s, **kw):
-            calls.append("region")
-            return _real(*args, **kw)
+        def __getattr__(self, name):
+            return getattr(real_ops(), name)
 
-        monkeypatch.setattr(mod, "fused_swin_attention_windows", spy_w)
-        monkeypatch.setattr(mod, "fused_swin_attention_shifted", spy_s)
+    spy_ops = OpsSpy()
+    monkeypatch.setattr(_native, "ops", lambda: spy_ops)
+    for mod, names in ((monai_patch, ("fused_swin_attention_windows", "fused_swin_attention_shifted")),
+                       (fused_block, ("fused_swin_attention_windows",))):
+        for name in names:
+            real = getattr(mod, name)
+            tag = "region" if name.endswith("shifted") else None
+
+            def spy(*args, _real=real, _tag=tag, **kw):
+                calls.append(_tag or ("tensor" if args[4] is not None else "none"))
+                return _real(*args, **kw)
+
+            monkeypatch.setattr(mod, name, spy)
     layer = _layer(48, 3, 4).to(dev).eval()
     x = torch.randn((1, 48, 14, 14, 14), device=dev)
     assert crumpet_amd.patch_monai_swin_unetr()
     _run(layer, x)
-    assert calls == ["none", "region"]  # block 0 has no shift; block 1 reads no mask
+    # block 0 has no shift; block 1 reads no mask
+    assert calls == (["msa-none", "msa-region"] if fused_block_on else ["none", "region"])
 
 
 def test_block_with_foreign_mask_uses_tensor_mask(patched, dev):

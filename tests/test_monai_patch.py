@@ -123,12 +123,20 @@ def test_module_cache_follows_parameter_updates():
     # a smaller window (the 6^3 stage rule) is a separate entry
     assert monai_patch._window_bias(attn, 216).shape == (3, 216, 216)
 
-    w, b = monai_patch._cast_linear(attn.qkv, torch.float16)
+    # the fused block's entry: bias and both projections in the compute dtype
+    bias, (w, b), (wp, bp) = monai_patch._block_params(attn, 343, torch.float16)
+    assert torch.equal(bias, second)
     assert w.dtype == torch.float16 and w.is_contiguous() and torch.equal(w, attn.qkv.weight.half())
-    assert monai_patch._cast_linear(attn.qkv, torch.float16)[0] is w
+    assert torch.equal(bp, attn.proj.bias.half())
+    again = monai_patch._block_params(attn, 343, torch.float16)
+    assert again[1][0] is w and again[0] is bias
     attn.qkv.weight = torch.nn.Parameter(torch.zeros_like(attn.qkv.weight))  # replaced: new storage
-    w2, _ = monai_patch._cast_linear(attn.qkv, torch.float16)
+    _, (w2, _), _ = monai_patch._block_params(attn, 343, torch.float16)
     assert w2 is not w and not w2.any()
+    with torch.no_grad():
+        attn.proj.bias.mul_(2.0)  # in place: version bump
+    _, _, (_, bp2) = monai_patch._block_params(attn, 343, torch.float16)
+    assert torch.equal(bp2, attn.proj.bias.half())
     # the compute dtype equal to the parameters' returns them as they are
-    w3, b3 = monai_patch._cast_linear(attn.proj, torch.float32)
-    assert w3 is attn.proj.weight and b3 is attn.proj.bias
+    _, (w3, b3), _ = monai_patch._block_params(attn, 343, torch.float32)
+    assert w3 is attn.qkv.weight and b3 is attn.qkv.bias
