@@ -282,6 +282,11 @@ def bench_attention(args, dev):
         t = views[i % R]
         ops.fused_swin_attention(ovs[i % R], t[0], t[1], t[2], bias, mask, bnd, 0.25)
 
+    # The first hundred or so attention launches of a process run up to 7%
+    # slower than the rest (measured: whichever of these calls is timed
+    # first, even after a 1 s clock settle), so an untimed pre-pass of 200
+    # launches (about 30 ms) comes before the first timing.
+    _events_time(attn, 200)
     t_attn = _steady_time(attn, args.warmup, args.steps, dev)
     t_shift = _steady_time(attn_shifted, args.warmup, args.steps, dev)
     res = dict(t_attn=t_attn, t_shift=t_shift)
@@ -849,11 +854,15 @@ def profile_run(dev):
     from crumpet_amd.fused_attention import fused_swin_attention_shifted
 
     ops = torch.ops.crumpet_ops
-    n = 20
+    n = 100
     times = {}
     def timed(name, fn):
+        # the timing of bench.py's components: a clock settle, 10 untimed
+        # launches (the first loads the code object), 100 timed (an
+        # attention kernel's first 20 launches after the settle ran about
+        # 4% faster than its 100-launch average)
         _settle_clock(dev)
-        for i in range(2):  # the first launches load the code object
+        for i in range(10):
             fn(i)
         times[name] = round(_events_time(fn, n) * 1e3, 2)
     B, D, H, W, C, ws, ss = (C1[k] for k in ("B", "D", "H", "W", "C", "ws", "ss"))
@@ -876,37 +885,45 @@ def profile_run(dev):
 
     qkvs, bias, mask, bnd = c3_inputs(dev, 3)
     Bw, Hh, N, Dh = C3["B"], C3["H"], C3["N"], C3["Dh"]
-    o = torch.empty((Bw, N, Hh * Dh), dtype=torch.float16, device=dev)
-    ov = o.view(Bw, N, Hh, Dh).permute(0, 2, 1, 3)
+    # three rotating input and output sets, as bench_attention times them
+    # (one output buffer rewritten by every launch stays partly in the MALL
+    # and read about 4% faster)
+    os_ = [torch.empty((Bw, N, Hh * Dh), dtype=torch.float16, device=dev) for _ in range(3)]
+    ovs = [o.view(Bw, N, Hh, Dh).permute(0, 2, 1, 3) for o in os_]
     views = [q.reshape(Bw, N, 3, Hh, Dh).permute(2, 0, 3, 1, 4) for q in qkvs]
     # the tensor-mask kernel reading the mask itself, then its tiled copy
     # (what fused_swin_attention_windows does from its second call with a
     # mask; the copy is made once here, outside the timed launches)
     from crumpet_amd.fused_attention import mask_tiles
 
-    timed("attention_tensor_mask_row_major",
-          lambda i: ops.fused_swin_attention(ov, views[i % 3][0], views[i % 3][1], views[i % 3][2], bias, mask,
-                                             bnd, 0.25))
+    def att(i, *extra):
+        t = views[i % 3]
+        return (ovs[i % 3], t[0], t[1], t[2], bias) + extra
+
+    # untimed pre-pass: the first hundred or so attention launches of a
+    # process run slower (see bench_attention); the profile summaries take
+    # each kernel's last 20 launches, the timed ones
+    for i in range(200):
+        ops.fused_swin_attention(*att(i, mask, bnd, 0.25))
+    timed("attention_tensor_mask_row_major", lambda i: ops.fused_swin_attention(*att(i, mask, bnd, 0.25)))
     tiles = mask_tiles(mask)
-    timed("attention_tensor_mask",
-          lambda i: ops.fused_swin_attention_tiled(ov, views[i % 3][0], views[i % 3][1], views[i % 3][2], bias,
-                                                   mask, tiles, bnd, 0.25))
+    timed("attention_tensor_mask", lambda i: ops.fused_swin_attention_tiled(*att(i, mask, tiles, bnd, 0.25)))
     del tiles
     vol = (C3["D"],) * 3
     timed("attention_shifted",
           lambda i: fused_swin_attention_shifted(views[i % 3][0], views[i % 3][1], views[i % 3][2], bias, vol,
-                                                 (7, 7, 7), (3, 3, 3), 0.25, ov))
-    del qkvs, views, o, ov, mask
+                                                 (7, 7, 7), (3, 3, 3), 0.25, ovs[i % 3]))
+    del qkvs, views, os_, ovs, mask
     # head dim 32 at the same window shape, shifted mode (the tuned kernel's
-    # strip-group form)
+    # strip-group form); two rotating input and output sets
     qkvs = [seeded((Bw, N, 3 * Hh * 32), torch.float16, 320 + r).to(dev) for r in range(2)]
     views = [q.reshape(Bw, N, 3, Hh, 32).permute(2, 0, 3, 1, 4) for q in qkvs]
-    o = torch.empty((Bw, N, Hh * 32), dtype=torch.float16, device=dev)
-    ov = o.view(Bw, N, Hh, 32).permute(0, 2, 1, 3)
+    os_ = [torch.empty((Bw, N, Hh * 32), dtype=torch.float16, device=dev) for _ in range(2)]
+    ovs = [o.view(Bw, N, Hh, 32).permute(0, 2, 1, 3) for o in os_]
     timed("attention_hd32_shifted",
           lambda i: fused_swin_attention_shifted(views[i % 2][0], views[i % 2][1], views[i % 2][2], bias, vol,
-                                                 (7, 7, 7), (3, 3, 3), 0.25, ov))
-    del qkvs, views, o, ov
+                                                 (7, 7, 7), (3, 3, 3), 0.25, ovs[i % 2]))
+    del qkvs, views, os_, ovs
 
     # fused block projections at the config-5 stage-0 shape: fp32 block
     # input [4,48^3,48] -> fp16 qkv [1372,343,144]; fp16 attention output
