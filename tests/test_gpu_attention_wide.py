@@ -262,22 +262,34 @@ def patched():
 def test_patched_basic_layer_head_dim_32(patched, dev, monkeypatch, fused_block, dim):
     """Feature size 96 or 192 with 3 heads (head dim 32 or 64): the patched
     BasicLayer (shifted and unshifted blocks) matches its own eager fp32
-    forward, through the fused block kernels and through partition /
-    attention / unpartition, both on the general kernel."""
-    from crumpet_amd import fused_block as fb
+    forward, through the fused block kernels (one window_msa_3d call per
+    block) and through partition / attention / unpartition, both on the
+    general kernel."""
+    from crumpet_amd import _native
     from crumpet_amd import monai_patch
 
     monkeypatch.setenv("CRUMPET_DISABLE_FUSED_BLOCK", fused_block)
     calls = []
-    for mod in (monai_patch, fb):
-        for name in ("fused_swin_attention_windows", "fused_swin_attention_shifted"):
-            real = getattr(mod, name)
+    real_ops = _native.ops
 
-            def spy(*args, _real=real, _name=name, **kw):
-                calls.append(_name)
-                return _real(*args, **kw)
+    class OpsSpy:
+        def window_msa_3d(self, *args):
+            calls.append("window_msa_3d(shift)" if any(args[-3:]) else "window_msa_3d(no shift)")
+            return real_ops().window_msa_3d(*args)
 
-            monkeypatch.setattr(mod, name, spy)
+        def __getattr__(self, name):
+            return getattr(real_ops(), name)
+
+    spy_ops = OpsSpy()
+    monkeypatch.setattr(_native, "ops", lambda: spy_ops)
+    for name in ("fused_swin_attention_windows", "fused_swin_attention_shifted"):
+        real = getattr(monai_patch, name)
+
+        def spy(*args, _real=real, _name=name, **kw):
+            calls.append(_name)
+            return _real(*args, **kw)
+
+        monkeypatch.setattr(monai_patch, name, spy)
     torch.manual_seed(3600)
     layer = sw.BasicLayer(dim=dim, depth=2, num_heads=3, window_size=(7, 7, 7), drop_path=0.0, qkv_bias=True,
                           downsample=None).to(dev).eval()
@@ -288,7 +300,10 @@ def test_patched_basic_layer_head_dim_32(patched, dev, monkeypatch, fused_block,
         got = layer(x)
     err = (got - want).abs().max().item()
     print(f"head dim {dim // 3} basic layer: max-abs {err:.2e}, kernel calls {calls}", flush=True)
-    assert calls == ["fused_swin_attention_windows", "fused_swin_attention_shifted"]
+    if fused_block == "0":
+        assert calls == ["window_msa_3d(no shift)", "window_msa_3d(shift)"]
+    else:
+        assert calls == ["fused_swin_attention_windows", "fused_swin_attention_shifted"]
     assert err < 1e-4
 
 
