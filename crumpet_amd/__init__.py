@@ -20,6 +20,7 @@ fallback: a tensor on another device, or a missing extension, raises
 from __future__ import annotations
 
 import contextlib
+import functools
 import os
 from typing import Sequence
 
@@ -58,6 +59,22 @@ def _op_range(name: str):
             or not torch.cuda.is_available()):
         return contextlib.nullcontext()
     return _RoctxRange(name)
+
+
+@functools.lru_cache(maxsize=256)
+def _checked_grid(D, H, W, window_size, shift_size) -> WindowGrid:
+    return WindowGrid.checked(D, H, W, window_size, shift_size)
+
+
+def _grid(D: int, H: int, W: int, window_size, shift_size) -> WindowGrid:
+    """``WindowGrid.checked``, kept for hashable arguments: the deep Swin
+    stages are host-bound, and validating the same geometry on every call
+    was about half of a gather call's Python time.  Invalid arguments raise
+    every time (exceptions are not cached); lists are validated each call."""
+    try:
+        return _checked_grid(D, H, W, window_size, shift_size)
+    except TypeError:  # unhashable window / shift sizes
+        return WindowGrid.checked(D, H, W, window_size, shift_size)
 
 
 def _device_ops(device: torch.device, what: str):
@@ -156,11 +173,9 @@ def fused_shift_partition_3d(
     """
     if x.ndim != 5:
         raise ValueError("x must have shape [B, D, H, W, C]")
-    window_size = as_triple("window_size", window_size)
-    shift_size = as_triple("shift_size", shift_size)
     require_float_dtype(x.dtype)
-    batch, D, H, W, channels = (int(v) for v in x.shape)
-    grid = WindowGrid.checked(D, H, W, window_size, shift_size)
+    batch, D, H, W, channels = map(int, x.shape)
+    grid = _grid(D, H, W, window_size, shift_size)
     if x.device.type == "meta":
         return x.new_empty(grid.windows_shape(batch, channels))
     _device_ops(x.device, "fused_shift_partition_3d")
@@ -186,13 +201,11 @@ def fused_unshift_unpartition_3d(
     """
     if windows.ndim != 3:
         raise ValueError("windows must have shape [B * num_windows, window_volume, C]")
-    window_size = as_triple("window_size", window_size)
-    shift_size = as_triple("shift_size", shift_size)
     require_float_dtype(windows.dtype)
-    grid = WindowGrid.checked(D, H, W, window_size, shift_size)
+    grid = _grid(D, H, W, window_size, shift_size)
     batch, channels = int(B), int(C)
     expected = grid.windows_shape(batch, channels)
-    if tuple(int(v) for v in windows.shape) != expected:
+    if tuple(map(int, windows.shape)) != expected:
         raise ValueError(f"windows must have shape {expected}")
     if windows.device.type == "meta":
         return windows.new_empty(grid.volume_shape(batch, channels))
