@@ -1148,10 +1148,10 @@ struct NoIssue {
 };
 
 // One strip's normalised output, held back for a deferred store (vector IO,
-// head dim 16): a wave writes window i's output at the top of window i + 1.
-// The vector-memory counter retires stores with the loads, so a store issued
-// at the end of window i would be waited for by the wait on window i + 1's
-// rows that ends the window; issued a window earlier it has long completed.
+// head dim 16): a wave writes window i's output after the wait on window
+// i + 1's rows that ends window i.  The vector-memory counter retires stores
+// with the loads, so a store issued before that wait would be waited for by
+// it; issued after it, the store completes during window i + 1.
 template <typename T>
 struct PendingOut {
     typename Frag<T>::x4 r;  // O[qi][4g .. 4g + 3]
@@ -1915,9 +1915,8 @@ swin_attention_tuned_kernel(const Params p) {
     if constexpr (kQReg) {
         // Head dim 16 on the LDS-DMA path: while window i is computed, its DMA
         // rounds bring in window i + 1's K and V, and Q travels by register
-        // (load_qraw at the window top, q_operand after the end-of-window
-        // wait).  A window's output is stored at the next window's top
-        // (PendingOut).
+        // (load_qraw a window ahead, q_operand after the end-of-window wait).
+        // A window's output is stored after that wait (PendingOut).
         // the window being computed (b0, code0, flag0: tensor mode reads its
         // mask) and the next one (b1, ...), as plain scalars: a struct here
         // was kept in memory, which the compiler placed in LDS
