@@ -70,7 +70,10 @@ def _grid(D: int, H: int, W: int, window_size, shift_size) -> WindowGrid:
     """``WindowGrid.checked``, kept for hashable arguments: the deep Swin
     stages are host-bound, and validating the same geometry on every call
     was about half of a gather call's Python time.  Invalid arguments raise
-    every time (exceptions are not cached); lists are validated each call."""
+    every time (exceptions are not cached); lists are validated each call,
+    and so is everything under torch.compile, which traces the check."""
+    if torch.compiler.is_compiling():
+        return WindowGrid.checked(D, H, W, window_size, shift_size)
     try:
         return _checked_grid(D, H, W, window_size, shift_size)
     except TypeError:  # unhashable window / shift sizes
