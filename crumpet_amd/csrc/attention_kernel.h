@@ -1428,7 +1428,10 @@ __device__ __forceinline__ bool attend_offset(const Params& p, const f32x4 (&bs)
         // register budget above 168 left after the bias tiles (not at 32 tiles)
         constexpr bool kWide = waves_per_eu<T, NT, kMask, kVec>() < 3 && NT <= 22;
         constexpr int kKAhead = (kUseMask && !kWide) ? 1 : 2;
-        constexpr int kMaskAhead = kWide ? 2 : 1;  // pairs
+        // the tiled mask copy (2 words per tile) at head dim 16, one head per
+        // workgroup: two pairs ahead fits the registers (168) and hides more
+        // of the loads (config 3: 153-154 -> 147-150 us)
+        constexpr int kMaskAhead = (kWide || (mask_tiled(kMask) && !kRec && D == 16)) ? 2 : 1;  // pairs
         X8 kf[NT];
         f32x4 S[NT];
         MaskWords mw[kUseMask ? NT : 1];
