@@ -55,6 +55,26 @@ def test_other_validation_errors():
                                                  (7, 7, 7), (3, 3, 3))
 
 
+def test_validated_grid_reuse():
+    """The gather wrappers keep each validated window grid: a repeated valid
+    geometry returns the same grid, an invalid one raises on every call
+    (after a valid call with the same window too), and list arguments, which
+    cannot be kept, give an equal grid."""
+    from crumpet_amd import _grid
+
+    first = _grid(14, 14, 14, (7, 7, 7), (3, 3, 3))
+    assert _grid(14, 14, 14, (7, 7, 7), (3, 3, 3)) is first
+    assert _grid(14, 14, 14, [7, 7, 7], [3, 3, 3]) == first
+    for _ in range(2):
+        with pytest.raises(ValueError, match="divisible"):
+            _grid(14, 14, 13, (7, 7, 7), (3, 3, 3))
+        with pytest.raises(ValueError, match="shift_size"):
+            _grid(14, 14, 14, (7, 7, 7), (3, 7, 3))
+    x = torch.empty((2, 14, 14, 14, 48), device="meta", dtype=torch.float16)
+    for ws, ss in (((7, 7, 7), (3, 3, 3)), ([7, 7, 7], [3, 3, 3])):
+        assert crumpet_amd.fused_shift_partition_3d(x, ws, ss).shape == (16, 343, 48)
+
+
 def test_meta_shape_propagation():
     x = torch.empty((2, 14, 14, 14, 48), device="meta", dtype=torch.float16)
     windows = crumpet_amd.fused_shift_partition_3d(x, (7, 7, 7), (3, 3, 3))
